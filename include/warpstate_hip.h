@@ -1,0 +1,167 @@
+/*
+ * warpstate_hip.h -- C ABI of the MI355X (gfx950) BF16 matmul hot path of WarpState.
+ *
+ * Every entry point takes raw device pointers, element strides and sizes, plus the
+ * hipStream_t to launch on (passed as void*; from Python it is
+ * torch.cuda.current_stream().cuda_stream of the calling thread). The library launches
+ * work on that stream and returns; it never allocates, frees or synchronises. The caller
+ * allocates every output and workspace. Outputs must not alias inputs; the FP32
+ * gradient buffer of ws_mm_accumulate_f32 is the only in-place operand.
+ *
+ * Return value: 0 on success, 1 for an invalid argument (nothing was launched), 2 for a
+ * HIP runtime error. ws_last_error() returns the calling thread's last message.
+ *
+ * Numerics: BF16 operands, FP32 accumulation in MFMA, BF16 round-to-nearest-even
+ * outputs, at the rounding points of the reference's PyTorch path.
+ *
+ * `algorithm` (GEMM entry points): 0 = "tiled" (one workgroup per output tile),
+ * 1 = "persistent" (one resident workgroup per CU slot striding over tiles),
+ * 2 = "persistent_tma" (persistent, with the reference's TMA preconditions checked by the
+ * caller). `tile`: 0 = 256x256 macro-tile (8 waves), 1 = 128x128 macro-tile (4 waves).
+ *
+ * Reference citations are path:line in gtausa197-svg/WarpState-AI.
+ */
+#ifndef WARPSTATE_HIP_H
+#define WARPSTATE_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Last error message of the calling thread ("" if none). */
+const char* ws_last_error(void);
+
+/* Library version string. */
+const char* ws_version(void);
+
+/*
+ * C[m,n] = bf16(A[m,k] @ B[k,n]), C row-contiguous with leading dimension n.
+ * A element (i,j) at a + i*a_s0 + j*a_s1, B element (i,j) at b + i*b_s0 + j*b_s1; any
+ * positive strides. Replaces the kernel launches of launch_mm
+ * (ops/matmul_kernels.py:167-205): `_matmul_kernel` (:81-108) for "tiled"/"persistent"
+ * and `warpstate::persistent_tma_mm` (:135-159) for "persistent_tma".
+ */
+int ws_mm(const void* a, int64_t a_s0, int64_t a_s1, const void* b, int64_t b_s0, int64_t b_s1,
+          void* c, int64_t m, int64_t n, int64_t k, int algorithm, int tile, void* stream);
+
+/*
+ * Paired up/gate projection with SwiGLU epilogue: packed[m, 2h] = bf16(A @ B) (up in
+ * columns [0,h), gate in [h,2h)), act[m,h] = bf16(r?(silu(gate)) * up), where silu runs
+ * on the BF16-rounded gate and is itself rounded iff eager_rounding. Replaces the launch
+ * of `_paired_swiglu_mm_kernel` in launch_swiglu_mm (ops/matmul_epilogue.py:86-142).
+ */
+int ws_swiglu_mm(const void* a, int64_t a_s0, int64_t a_s1, const void* b, int64_t b_s0,
+                 int64_t b_s1, void* packed, void* act, int64_t m, int64_t h, int64_t k,
+                 int eager_rounding, int algorithm, int tile, void* stream);
+
+/* Standalone SwiGLU of a contiguous packed [rows, 2h] BF16 projection; replaces
+ * bf16_swiglu (ops/activation_execution.py:58-70). */
+int ws_swiglu_forward(const void* packed, void* out, int64_t rows, int64_t h, int eager_rounding,
+                      void* stream);
+
+/* SwiGLU backward: out[rows, 2h] = (dUp | dGate) from packed [rows, 2h] and contiguous
+ * grad [rows, h]; replaces `_swiglu_backward` (ops/activation_execution.py:73-81). */
+int ws_swiglu_backward(const void* packed, const void* grad, void* out, int64_t rows, int64_t h,
+                       int eager_rounding, void* stream);
+
+/* BF16 RMSNorm forward of contiguous x [rows, d] with FP32 weight; writes y and the FP32
+ * row rsqrt; replaces bf16_rmsnorm (ops/activation_execution.py:161-173). */
+int ws_rmsnorm_forward(const void* x, const float* weight, void* y, float* rstd, int64_t rows,
+                       int64_t d, float eps, int eager_rounding, void* stream);
+
+/* Floats of the `partial` workspace ws_rmsnorm_backward needs. */
+int64_t ws_rmsnorm_backward_partial_floats(int64_t rows, int64_t d);
+
+/* RMSNorm backward: dx [rows, d] BF16 and dweight [d] FP32 from x, weight, rstd and a
+ * contiguous grad; replaces `_rms_backward` (ops/activation_execution.py:176-194). */
+int ws_rmsnorm_backward(const void* x, const float* weight, const float* rstd, const void* grad,
+                        void* dx, float* dweight, float* partial, int64_t rows, int64_t d,
+                        int eager_rounding, void* stream);
+
+/* Row statistics of RMSNorm: rstd[r] = 1/sqrt(mean_k f32(x[r,k])^2 + eps) for x with row
+ * stride ldx (warpstate/model.py:26-27). */
+int ws_rms_rstd(const void* x, int64_t ldx, float* rstd, int64_t rows, int64_t d, float eps,
+                void* stream);
+
+/*
+ * RMSNorm-prologue projection with gate sigmoid: out[m,n] = bf16(y @ B) where
+ * y = r(r(x * rstd) * r(norm_weight)) is formed in the GEMM's operand path and never
+ * stored, then out[:, gate_begin:gate_end] = r(sigmoid(out)). Also writes rstd [m].
+ * Restates RMSNorm.forward (warpstate/model.py:22-28) -> in_proj (warpstate/model.py:93,
+ * 109) -> torch.sigmoid on the gate slice (warpstate/model.py:174). x needs a unit
+ * column stride.
+ */
+int ws_rmsnorm_gate_mm(const void* x, int64_t x_s0, const float* norm_weight, float eps,
+                       float* rstd, const void* b, int64_t b_s0, int64_t b_s1, void* out,
+                       int64_t m, int64_t n, int64_t k, int64_t gate_begin, int64_t gate_end,
+                       void* stream);
+
+/* Down projection with residual add: out[m,n] = r(residual[m,n] + r(A @ B)), residual
+ * row stride ld_residual (warpstate/model.py:178 under BF16 residuals,
+ * ops/residual_experiment.py:25-58). */
+int ws_residual_mm(const void* a, int64_t a_s0, int64_t a_s1, const void* b, int64_t b_s0,
+                   int64_t b_s1, const void* residual, int64_t ld_residual, void* out, int64_t m,
+                   int64_t n, int64_t k, void* stream);
+
+/*
+ * Down-projection dgrad with SwiGLU-backward epilogue: dact = r(grad @ B) (grad [m,k] =
+ * dY, B [k,h] = W_down of nn.Linear layout [k,h]) is never stored; from the saved packed
+ * [m,2h] projection it writes dpacked [m,2h] = (dUp | dGate). Restates `_mm_backward`'s
+ * dX (ops/matmul_execution.py:239) followed by `_swiglu_backward_kernel`
+ * (ops/activation_execution.py:36-55).
+ */
+int ws_swiglu_backward_mm(const void* grad, int64_t g_s0, int64_t g_s1, const void* b,
+                          int64_t b_s0, int64_t b_s1, const void* packed, void* dpacked,
+                          int64_t m, int64_t h, int64_t k, int eager_rounding, void* stream);
+
+/* Floats of the workspace ws_mm_accumulate_f32 needs for `splits` split-K slices
+ * (0 when splits <= 1). */
+int64_t ws_mm_accumulate_workspace_floats(int64_t m, int64_t n, int64_t splits);
+
+/*
+ * Weight-gradient GEMM accumulated into an FP32 buffer: G[m,n] += f32(r(A @ B)) when
+ * round_bf16 (the BF16 dW then AccumulateGrad of test_gradient_execution.py:243-246 and
+ * ops/matmul_execution.py:243), or G += A @ B in FP32 otherwise (the "direct_fp32_addmm"
+ * variant of ops/benchmark_gradient_accumulation.py:141-144). splits > 1 reduces K in
+ * slices through `workspace`.
+ */
+int ws_mm_accumulate_f32(const void* a, int64_t a_s0, int64_t a_s1, const void* b, int64_t b_s0,
+                         int64_t b_s1, float* g, int64_t ldg, int64_t m, int64_t n, int64_t k,
+                         int round_bf16, float* workspace, int64_t splits, void* stream);
+
+/* Number of per-row partials (floats per row of part_max / part_sum) for `vocab`. */
+int64_t ws_linear_ce_parts(int64_t vocab);
+
+/*
+ * Fused LM-head cross-entropy forward. hidden [rows, d] (row stride ld_hidden, unit column
+ * stride), weight [vocab, d] (nn.Embedding / tied head layout, row stride ld_weight),
+ * int64 targets with -100 ignored. Writes per-token FP32 loss, lse, the target logit,
+ * mean = sum(loss) / max(1, count) and count; logits exist only in registers.
+ * Restates the chunked head of WarpStateLM.forward (warpstate/model.py:316-334) and
+ * `_full_loss` (ops/loss_experiment.py:14-19).
+ */
+int ws_linear_ce_forward(const void* hidden, int64_t ld_hidden, const void* weight,
+                         int64_t ld_weight, const int64_t* targets, int64_t rows, int64_t vocab,
+                         int64_t d, float* part_max, float* part_sum, float* target_logit,
+                         float* lse, float* loss, float* mean, float* count, void* stream);
+
+/*
+ * Fused LM-head cross-entropy backward: dhidden [rows, d] = r(r(g (softmax - onehot)) @ W)
+ * with g = grad_mean / max(1, count), zero rows for ignored targets. Logit gradients are
+ * formed chunk_rows rows at a time into grad_logits_ws [chunk_rows, vocab] BF16 and
+ * consumed by the dhidden GEMM of that chunk; scale_ws holds one float.
+ * Restates autograd of warpstate/model.py:321-334.
+ */
+int ws_linear_ce_backward(const void* hidden, int64_t ld_hidden, const void* weight,
+                          int64_t ld_weight, const int64_t* targets, const float* lse,
+                          const float* count, const float* grad_mean, int64_t rows,
+                          int64_t vocab, int64_t d, void* grad_logits_ws, int64_t chunk_rows,
+                          float* scale_ws, void* dhidden, int64_t ld_dhidden, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* WARPSTATE_HIP_H */

@@ -1,0 +1,278 @@
+"""GPU parity of the fused GEMMs against the CPU oracle at reduced sizes.
+
+* paired SwiGLU GEMM: test_matmul_epilogue.py:54-84 restated (shapes, tiles, schedules,
+  both roundings; projection vs FP32 dot; activation recomputed from the returned packed);
+* RMSNorm-prologue projection with gate sigmoid, residual epilogue, SwiGLU-backward
+  epilogue, FP32 weight-gradient accumulation (plain and split-K), the MLP backward, and
+  the fused LM-head cross-entropy (loss, mean, count, dHidden).
+Bars: BF16 max|d|/max|ref| <= 1e-2 and rel-RMS <= 3e-3; FP32 ||d||/||ref|| <= 1e-3;
+counts bit-exact.
+"""
+import math
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from metrics import assert_bf16_close, assert_f32_close, max_rel, rel_l2
+from oracle import reference as oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def _gen(seed):
+    return torch.Generator("cpu").manual_seed(seed)
+
+
+@pytest.mark.parametrize("algorithm", ["tiled", "persistent"])
+@pytest.mark.parametrize("eager_rounding", [False, True])
+@pytest.mark.parametrize("shape", [(13, 46, 31), (128, 256, 128), (257, 192, 193), (512, 1024, 256)])
+@pytest.mark.parametrize("tile", [(64, 64, 32, 4, 3), (128, 128, 32, 8, 3)])
+def test_swiglu_projection_and_activation(algorithm, eager_rounding, shape, tile):
+    from ops.matmul_epilogue import launch_swiglu_mm
+
+    m, packed_width, k = shape
+    gen = _gen(561)
+    a = (torch.randn(m, k, generator=gen) * 0.1).bfloat16()
+    b = (torch.randn(packed_width, k, generator=gen) * 0.1).bfloat16().T
+    packed, act = launch_swiglu_mm(a.cuda(), b.cuda(), algorithm, tile, eager_rounding)
+    torch.cuda.synchronize()
+    want_packed, want_act = oracle.swiglu_mm(a, b, eager_rounding)
+    assert packed.is_contiguous() and act.is_contiguous()
+    assert_bf16_close(packed, want_packed, "packed")
+    assert_bf16_close(act, want_act, "act")
+    accumulated = oracle.mm_f32_reference(a, b)
+    assert rel_l2(packed, accumulated) < 1e-3
+    # The activation must consume the returned rounded projection.
+    torch.testing.assert_close(act.cpu(), oracle.swiglu(packed.cpu(), eager_rounding),
+                               rtol=0.01, atol=2e-4)
+
+
+def test_swiglu_zero_gate_weights_give_exact_zero():
+    from ops.matmul_epilogue import launch_swiglu_mm
+
+    gen = _gen(3)
+    a = torch.randn(256, 128, generator=gen).bfloat16()
+    w = torch.randn(512, 128, generator=gen).bfloat16()
+    w[256:] = 0  # gate half
+    packed, act = launch_swiglu_mm(a.cuda(), w.cuda().T, "tiled", (128, 128, 32, 8, 3), True)
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(act).item() == 0
+    assert torch.count_nonzero(packed[:, 256:]).item() == 0
+
+
+@pytest.mark.parametrize("m,d,n,gate", [(512, 256, 576, (384, 512)), (300, 2048, 1152, (768, 1024)),
+                                        (1024, 2048, 9216, (6144, 8192))])
+def test_rmsnorm_gate_projection(m, d, n, gate):
+    from ops.benchmark_configs import rms_projection_inputs
+    from ops.fused_execution import rmsnorm_gate_mm
+
+    inp = rms_projection_inputs(m=m, d=d, n=n, gate=gate, seed=0)
+    out, rstd = rmsnorm_gate_mm(inp["x"].cuda(), inp["norm_weight"].cuda(), inp["eps"],
+                                inp["w"].cuda(), gate)
+    torch.cuda.synchronize()
+    want = oracle.rmsnorm_gate_projection(inp["x"], inp["norm_weight"], inp["eps"], inp["w"], gate)
+    assert_bf16_close(out, want, "rms gate projection")
+    assert_f32_close(rstd.cpu(), oracle.rms_rstd(inp["x"], inp["eps"]), "rstd")
+    gate_vals = out[:, gate[0]:gate[1]].float()
+    assert gate_vals.min().item() >= 0.0 and gate_vals.max().item() <= 1.0
+
+
+def test_rmsnorm_gate_zero_weight_is_half_on_gate():
+    from ops.fused_execution import rmsnorm_gate_mm
+
+    gen = _gen(9)
+    x = torch.randn(256, 512, generator=gen).bfloat16().cuda()
+    w = torch.zeros(640, 512, dtype=torch.bfloat16, device="cuda")
+    nw = torch.ones(512, device="cuda")
+    out, _ = rmsnorm_gate_mm(x, nw, 1e-6, w, (256, 384))
+    torch.cuda.synchronize()
+    expect = torch.zeros(256, 640)
+    expect[:, 256:384] = 0.5
+    assert torch.equal(out.float().cpu(), expect)
+
+
+@pytest.mark.parametrize("m,ffn,d", [(512, 1408, 512), (300, 5632, 2048), (64, 200, 72)])
+def test_residual_projection(m, ffn, d):
+    from ops.benchmark_configs import down_residual_inputs
+    from ops.fused_execution import residual_mm
+
+    inp = down_residual_inputs(m=m, ffn=ffn, d=d, seed=0)
+    out = residual_mm(inp["h"].cuda(), inp["w_down"].cuda(), inp["residual"].cuda())
+    torch.cuda.synchronize()
+    assert_bf16_close(out, oracle.residual_projection(inp["h"], inp["w_down"], inp["residual"]),
+                      "residual")
+
+
+def test_residual_zero_weight_returns_residual_bitwise():
+    from ops.fused_execution import residual_mm
+
+    gen = _gen(4)
+    h = torch.randn(384, 640, generator=gen).bfloat16().cuda()
+    r = torch.randn(384, 512, generator=gen).bfloat16().cuda()
+    out = residual_mm(h, torch.zeros(512, 640, dtype=torch.bfloat16, device="cuda"), r)
+    torch.cuda.synchronize()
+    assert torch.equal(out, r)
+
+
+def _mlp_case(m, d, ffn, seed=0):
+    from ops.benchmark_configs import mlp_backward_inputs
+
+    inp = mlp_backward_inputs(m=m, d=d, ffn=ffn, seed=seed)
+    packed, act = oracle.swiglu_mm(inp["x"], inp["w_upgate"].T, True)
+    return inp, packed, act
+
+
+@pytest.mark.parametrize("eager_rounding", [True, False])
+@pytest.mark.parametrize("m,d,ffn", [(512, 512, 704), (256, 2048, 1408), (100, 72, 40)])
+def test_swiglu_backward_epilogue(eager_rounding, m, d, ffn):
+    from ops.fused_execution import swiglu_backward_mm
+
+    inp, packed, _act = _mlp_case(m, d, ffn)
+    dpacked = swiglu_backward_mm(inp["dy"].cuda(), inp["w_down"].cuda(), packed.cuda(),
+                                 eager_rounding)
+    torch.cuda.synchronize()
+    dact = oracle.mm(inp["dy"], inp["w_down"])
+    want = oracle.swiglu_backward(packed, dact, eager_rounding)
+    assert_bf16_close(dpacked[:, :ffn], want[:, :ffn], "dUp")
+    assert_bf16_close(dpacked[:, ffn:], want[:, ffn:], "dGate")
+
+
+@pytest.mark.parametrize("splits", [1, 3])
+@pytest.mark.parametrize("layout", ["dw", "nn", "nt"])
+def test_weight_gradient_fp32_accumulation(splits, layout):
+    from ops.fused_execution import mm_accumulate_
+
+    gen = _gen(901)
+    tokens, n_out, n_in = 1024, 384, 320
+    dy = torch.randn(tokens, n_out, generator=gen).bfloat16()
+    x = torch.randn(tokens, n_in, generator=gen).bfloat16()
+    g = torch.randn(n_out, n_in, generator=gen) * 1e-2
+    if layout == "dw":
+        a, b = dy.T, x
+    elif layout == "nn":
+        a, b = dy.T.contiguous(), x
+    else:
+        a, b = dy.T.contiguous(), x.T.contiguous().T
+    ga, gb = a.cuda(), b.cuda()
+    assert ga.stride() == a.stride() and gb.stride() == b.stride()
+    gg = g.cuda()
+    mm_accumulate_(gg, ga, gb, True, splits)
+    torch.cuda.synchronize()
+    assert_f32_close(gg.cpu(), oracle.accumulate_weight_grad(g, a, b), f"{layout} splits={splits}")
+
+
+def test_weight_gradient_zero_upstream_leaves_buffer_bitwise():
+    from ops.fused_execution import mm_accumulate_
+
+    gen = _gen(2)
+    g = torch.randn(256, 192, generator=gen).cuda()
+    before = g.clone()
+    x = torch.randn(512, 192, generator=gen).bfloat16().cuda()
+    mm_accumulate_(g, torch.zeros(512, 256, dtype=torch.bfloat16, device="cuda").T, x)
+    torch.cuda.synchronize()
+    assert torch.equal(g, before)
+
+
+def test_mlp_backward_matches_oracle():
+    from ops.fused_execution import mlp_backward
+
+    m, d, ffn = 512, 256, 352
+    inp, packed, act = _mlp_case(m, d, ffn)
+    g_up, g_down = inp["g_upgate"].cuda(), inp["g_down"].cuda()
+    dx = mlp_backward(inp["x"].cuda(), inp["w_upgate"].cuda(), inp["w_down"].cuda(),
+                      packed.cuda(), act.cuda(), inp["dy"].cuda(), g_up, g_down)
+    torch.cuda.synchronize()
+    want_dx, _dp, want_gup, want_gdown = oracle.mlp_backward(
+        inp["x"], inp["w_upgate"], inp["w_down"], packed, act, inp["dy"],
+        inp["g_upgate"], inp["g_down"])
+    assert_bf16_close(dx, want_dx, "dX")
+    assert_f32_close(g_up.cpu(), want_gup, "G_upgate")
+    assert_f32_close(g_down.cpu(), want_gdown, "G_down")
+
+
+@pytest.mark.parametrize("m,d,vocab,chunk", [(512, 256, 1024, 2048), (300, 512, 4096, 128),
+                                             (1024, 2048, 8192, 512)])
+def test_linear_cross_entropy(m, d, vocab, chunk):
+    from ops.benchmark_configs import lm_head_inputs
+    from ops.fused_execution import CrossEntropyState, linear_cross_entropy_backward, \
+        linear_cross_entropy_forward
+
+    inp = lm_head_inputs(m=m, d=d, vocab=vocab, seed=0)
+    h, w, t = inp["hidden"].cuda(), inp["weight"].cuda(), inp["targets"].cuda()
+    state = CrossEntropyState(m, vocab, h.device, chunk_rows=chunk)
+    linear_cross_entropy_forward(h, w, t, state)
+    dh = linear_cross_entropy_backward(h, w, t, state, torch.ones((), device="cuda"))
+    torch.cuda.synchronize()
+    loss, mean, count, dhidden = oracle.linear_cross_entropy(inp["hidden"], inp["weight"],
+                                                             inp["targets"])
+    assert int(state.count.item()) == count
+    assert_f32_close(state.loss.cpu(), loss, "per-token loss")
+    assert abs(state.mean.item() - mean.item()) <= 1e-3 * abs(mean.item())
+    ignored = inp["targets"] == -100
+    assert torch.count_nonzero(state.loss.cpu()[ignored]).item() == 0
+    assert torch.count_nonzero(dh.cpu()[ignored]).item() == 0
+    assert_bf16_close(dh, dhidden, "dHidden")
+
+
+def test_linear_cross_entropy_zero_weight_and_all_ignored():
+    from ops.fused_execution import linear_cross_entropy_backward, linear_cross_entropy_forward
+
+    gen = _gen(12)
+    vocab = 2048
+    h = torch.randn(256, 128, generator=gen).bfloat16().cuda()
+    w = torch.zeros(vocab, 128, dtype=torch.bfloat16, device="cuda")
+    t = torch.randint(0, vocab, (256,), generator=gen).cuda()
+    state = linear_cross_entropy_forward(h, w, t)
+    dh = linear_cross_entropy_backward(h, w, t, state, torch.ones((), device="cuda"))
+    torch.cuda.synchronize()
+    assert torch.allclose(state.loss.cpu(), torch.full((256,), math.log(vocab)), rtol=1e-6, atol=1e-5)
+    assert torch.count_nonzero(dh).item() == 0
+    t_all = torch.full((256,), -100, dtype=torch.int64, device="cuda")
+    w2 = torch.randn(vocab, 128, generator=gen).bfloat16().cuda()
+    state = linear_cross_entropy_forward(h, w2, t_all)
+    dh = linear_cross_entropy_backward(h, w2, t_all, state, torch.ones((), device="cuda"))
+    torch.cuda.synchronize()
+    assert state.mean.item() == 0.0 and state.count.item() == 0.0
+    assert torch.count_nonzero(state.loss).item() == 0 and torch.count_nonzero(dh).item() == 0
+
+
+@pytest.mark.parametrize("shape", [(3, 224), (2, 32, 256), (257, 14336)])
+@pytest.mark.parametrize("eager_rounding", [True, False])
+def test_standalone_swiglu_forward_backward(shape, eager_rounding):
+    from ops.activation_execution import bf16_swiglu
+
+    gen = _gen(947)
+    source = torch.randn(shape, generator=gen).bfloat16()
+    actual = source.cuda().requires_grad_()
+    out = bf16_swiglu(actual, eager_rounding=eager_rounding)
+    grad = torch.randn(out.shape, generator=gen).bfloat16()
+    out.backward(grad.cuda())
+    torch.cuda.synchronize()
+    flat = source.reshape(-1, shape[-1])
+    assert_bf16_close(out.reshape(-1, shape[-1] // 2), oracle.swiglu(flat, eager_rounding), "swiglu")
+    want = oracle.swiglu_backward(flat, grad.reshape(-1, shape[-1] // 2), eager_rounding)
+    assert_bf16_close(actual.grad.reshape(-1, shape[-1]), want, "swiglu grad")
+
+
+@pytest.mark.parametrize("shape", [(3, 24), (2, 16, 128), (257, 2048)])
+def test_standalone_rmsnorm_forward_backward(shape):
+    from ops.activation_execution import bf16_rmsnorm
+
+    gen = _gen(949)
+    weight = torch.rand(shape[-1], generator=gen) * 1.9 + 0.1
+    source = torch.randn(shape, generator=gen).bfloat16()
+    x_ref = source.clone().requires_grad_()
+    w_ref = weight.clone().requires_grad_()
+    expected = oracle.rmsnorm(x_ref, w_ref, 1e-5)
+    grad = torch.randn(shape, generator=gen).bfloat16()
+    expected.backward(grad)
+    x = source.cuda().requires_grad_()
+    w = weight.cuda().requires_grad_()
+    out, rstd = bf16_rmsnorm(x, w, 1e-5, True)
+    out.backward(grad.cuda())
+    torch.cuda.synchronize()
+    assert_bf16_close(out, expected.detach(), "rmsnorm")
+    assert_bf16_close(x.grad, x_ref.grad, "rmsnorm dx")
+    assert w.grad.dtype == torch.float32
+    assert rel_l2(w.grad, w_ref.grad) <= 3e-3

@@ -1,0 +1,61 @@
+// Error reporting, device properties and per-device kernel attributes of the C ABI.
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/warpstate_hip.h"
+#include "launch.h"
+
+namespace ws {
+
+static thread_local std::string g_last_error;
+
+int set_error(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+static constexpr int kMaxDevices = 64;
+static std::mutex g_mu;
+static int g_cus[kMaxDevices];
+
+int device_cus() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 256;
+  std::lock_guard<std::mutex> lock(g_mu);
+  if (g_cus[dev] == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cus <= 0)
+      cus = 256;
+    g_cus[dev] = cus;
+  }
+  return g_cus[dev];
+}
+
+// hipFuncSetAttribute applies to the current device; remember (kernel, device) pairs.
+int ensure_lds(const void* kernel, int bytes) {
+  static std::mutex mu;
+  static std::vector<std::pair<const void*, int>>* seen = new std::vector<std::pair<const void*, int>>();
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return set_error(kHipError, "hipGetDevice failed");
+  std::lock_guard<std::mutex> lock(mu);
+  for (auto& e : *seen)
+    if (e.first == kernel && e.second == dev) return kOk;
+  hipError_t err = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  if (err != hipSuccess)
+    return set_error(kHipError, "hipFuncSetAttribute(%d bytes LDS): %s", bytes, hipGetErrorString(err));
+  seen->push_back({kernel, dev});
+  return kOk;
+}
+
+}  // namespace ws
+
+extern "C" const char* ws_last_error(void) { return ws::g_last_error.c_str(); }
+
+extern "C" const char* ws_version(void) { return "warpstate-hip 0.1 gfx950"; }

@@ -1,0 +1,153 @@
+// C ABI: fused GEMMs of the forward and backward MLP / attention-input projections.
+#include "../../include/warpstate_hip.h"
+#include "launch.h"
+#include "rowops.h"
+
+namespace ws {
+int check_gemm_args(const void* a, long a_s0, long a_s1, const void* b, long b_s0, long b_s1,
+                    const void* c, long m, long n, long k);
+int operand_mode(const OperandDesc& d, long rows, long k, int tile_rows);
+}  // namespace ws
+
+using namespace ws;
+
+static inline OperandDesc desc_a(const void* a, long s0, long s1) {
+  return OperandDesc{static_cast<const unsigned short*>(a), s0, s1};
+}
+static inline OperandDesc desc_b(const void* b, long s0, long s1) {
+  return OperandDesc{static_cast<const unsigned short*>(b), s1, s0};
+}
+static inline bool al(const void* p, int bytes) {
+  return reinterpret_cast<unsigned long>(p) % bytes == 0;
+}
+
+static int launch_rstd(const void* x, long ldx, float* rstd, long rows, long d, float eps,
+                       hipStream_t s) {
+  const int vec = (ldx % 8 == 0) && (d % 8 == 0) && al(x, 16);
+  hipLaunchKernelGGL(rms_rstd_kernel, dim3(cdiv(rows, 4)), dim3(256), 0, s,
+                     static_cast<const unsigned short*>(x), ldx, rstd, (int)rows, (int)d, eps, vec);
+  return hip_check(hipGetLastError(), "rms_rstd launch");
+}
+
+extern "C" int ws_rms_rstd(const void* x, int64_t ldx, float* rstd, int64_t rows, int64_t d,
+                           float eps, void* stream) {
+  if (!x || !rstd) return set_error(kInvalid, "null pointer");
+  if (rows < 1 || d < 1 || !fits_i32(rows) || !fits_i32(d) || ldx < d)
+    return set_error(kInvalid, "invalid RMSNorm shape");
+  return launch_rstd(x, ldx, rstd, rows, d, eps, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int ws_rmsnorm_gate_mm(const void* x, int64_t x_s0, const float* norm_weight,
+                                  float eps, float* rstd, const void* b, int64_t b_s0,
+                                  int64_t b_s1, void* out, int64_t m, int64_t n, int64_t k,
+                                  int64_t gate_begin, int64_t gate_end, void* stream) {
+  if (int rc = check_gemm_args(x, x_s0, 1, b, b_s0, b_s1, out, m, n, k)) return rc;
+  if (!norm_weight || !rstd) return set_error(kInvalid, "null RMSNorm pointer");
+  if (gate_begin < 0 || gate_end < gate_begin || gate_end > n)
+    return set_error(kInvalid, "gate column range [%ld, %ld) outside [0, %ld)", (long)gate_begin,
+                     (long)gate_end, (long)n);
+  if (x_s0 < k) return set_error(kInvalid, "RMSNorm prologue needs row-contiguous x");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (int rc = launch_rstd(x, x_s0, rstd, m, k, eps, s)) return rc;
+  GemmParams p{};
+  p.a = desc_a(x, x_s0, 1);
+  p.b = desc_b(b, b_s0, b_s1);
+  p.M = (int)m; p.N = (int)n; p.K = (int)k;
+  p.c = static_cast<unsigned short*>(out);
+  p.ldc = n;
+  p.vec_out = (n % 4 == 0) && al(out, 8);
+  p.rstd = rstd;
+  p.norm_w = norm_weight;
+  p.gate_lo = (int)gate_begin;
+  p.gate_hi = (int)gate_end;
+  int am = operand_mode(p.a, m, k, 256);
+  if (am != kKContig)
+    return set_error(kInvalid, "RMSNorm prologue needs a 16-byte aligned x with k %% 8 == 0");
+  int bm = operand_mode(p.b, n, k, 256);
+  constexpr unsigned mask = kMaskKK | ab_bit(kKContig, kGeneric);
+  return dispatch<mask, WS_TILE_ARGS_LARGE, false, true, EpiStore<true, false>>(p, am, bm,
+                                                                                 LaunchCfg{0, 1}, s);
+}
+
+extern "C" int ws_residual_mm(const void* a, int64_t a_s0, int64_t a_s1, const void* b,
+                              int64_t b_s0, int64_t b_s1, const void* residual,
+                              int64_t ld_residual, void* out, int64_t m, int64_t n, int64_t k,
+                              void* stream) {
+  if (int rc = check_gemm_args(a, a_s0, a_s1, b, b_s0, b_s1, out, m, n, k)) return rc;
+  if (!residual || ld_residual < n) return set_error(kInvalid, "invalid residual operand");
+  GemmParams p{};
+  p.a = desc_a(a, a_s0, a_s1);
+  p.b = desc_b(b, b_s0, b_s1);
+  p.M = (int)m; p.N = (int)n; p.K = (int)k;
+  p.c = static_cast<unsigned short*>(out);
+  p.ldc = n;
+  p.aux = static_cast<const unsigned short*>(residual);
+  p.ldaux = ld_residual;
+  p.vec_out = (n % 4 == 0) && (ld_residual % 4 == 0) && al(out, 8) && al(residual, 8);
+  int am = operand_mode(p.a, m, k, 256), bm = operand_mode(p.b, n, k, 256);
+  constexpr unsigned mask = kMaskKK | ab_bit(kKContig, kMNContig) | kMaskGG;
+  return dispatch<mask, WS_TILE_ARGS_LARGE, false, false, EpiStore<false, true>>(
+      p, am, bm, LaunchCfg{0, 1}, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int ws_swiglu_backward_mm(const void* grad, int64_t g_s0, int64_t g_s1, const void* b,
+                                     int64_t b_s0, int64_t b_s1, const void* packed,
+                                     void* dpacked, int64_t m, int64_t h, int64_t k,
+                                     int eager_rounding, void* stream) {
+  if (int rc = check_gemm_args(grad, g_s0, g_s1, b, b_s0, b_s1, dpacked, m, h, k)) return rc;
+  if (!packed) return set_error(kInvalid, "null packed projection");
+  GemmParams p{};
+  p.a = desc_a(grad, g_s0, g_s1);
+  p.b = desc_b(b, b_s0, b_s1);
+  p.M = (int)m; p.N = (int)h; p.K = (int)k; p.H = (int)h;
+  p.c = static_cast<unsigned short*>(dpacked);
+  p.ldc = 2 * h;
+  p.aux = static_cast<const unsigned short*>(packed);
+  p.ldaux = 2 * h;
+  p.eager = eager_rounding ? 1 : 0;
+  p.vec_out = (h % 4 == 0) && al(dpacked, 8) && al(packed, 8);
+  int am = operand_mode(p.a, m, k, 256), bm = operand_mode(p.b, h, k, 256);
+  constexpr unsigned mask = kMaskKK | ab_bit(kKContig, kMNContig) | kMaskGG;
+  return dispatch<mask, WS_TILE_ARGS_LARGE, false, false, EpiSwigluBwd>(
+      p, am, bm, LaunchCfg{0, 1}, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int64_t ws_mm_accumulate_workspace_floats(int64_t m, int64_t n, int64_t splits) {
+  return splits <= 1 ? 0 : m * n * splits;
+}
+
+extern "C" int ws_mm_accumulate_f32(const void* a, int64_t a_s0, int64_t a_s1, const void* b,
+                                    int64_t b_s0, int64_t b_s1, float* g, int64_t ldg, int64_t m,
+                                    int64_t n, int64_t k, int round_bf16, float* workspace,
+                                    int64_t splits, void* stream) {
+  if (int rc = check_gemm_args(a, a_s0, a_s1, b, b_s0, b_s1, g, m, n, k)) return rc;
+  if (ldg < n) return set_error(kInvalid, "gradient leading dimension %ld < n", (long)ldg);
+  if (splits < 1 || splits > 64) return set_error(kInvalid, "splits must be in [1, 64]");
+  if (splits > 1 && !workspace) return set_error(kInvalid, "split-K needs a workspace");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  GemmParams p{};
+  p.a = desc_a(a, a_s0, a_s1);
+  p.b = desc_b(b, b_s0, b_s1);
+  p.M = (int)m; p.N = (int)n; p.K = (int)k;
+  p.round_acc = round_bf16 ? 1 : 0;
+  int am = operand_mode(p.a, m, k, 256), bm = operand_mode(p.b, n, k, 256);
+  if (splits <= 1) {
+    p.g = g;
+    p.ldg = ldg;
+    p.vec_out = (n % 4 == 0) && (ldg % 4 == 0) && al(g, 16);
+    return dispatch<kMaskMM, WS_TILE_ARGS_LARGE, false, false, EpiAccF32<false>>(p, am, bm,
+                                                                                  LaunchCfg{0, 1}, s);
+  }
+  p.g = workspace;
+  p.ldg = n;
+  p.split_stride = m * n;
+  p.vec_out = (n % 4 == 0) && al(workspace, 16);
+  if (int rc = dispatch<kMaskMM, WS_TILE_ARGS_LARGE, false, false, EpiAccF32<true>>(
+          p, am, bm, LaunchCfg{0, (int)splits}, s))
+    return rc;
+  long total = m * n;
+  hipLaunchKernelGGL(splitk_accum_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
+                     workspace, (int)splits, (long)(m * n), g, (long)ldg, (int)m, (int)n,
+                     round_bf16 ? 1 : 0);
+  return hip_check(hipGetLastError(), "split-K reduce launch");
+}

@@ -1,0 +1,277 @@
+// Row-wise and elementwise kernels of the hot path: RMSNorm statistics / forward /
+// backward, standalone SwiGLU forward / backward, cross-entropy reductions and
+// split-K reductions. All are HBM-bound; each reads and writes its operands once.
+#pragma once
+
+#include "common.h"
+
+namespace ws {
+
+// ---------------------------------------------------------------------------------------
+// RMSNorm row statistics: rstd[r] = 1 / sqrt(sum_k f32(x[r,k])^2 / D + eps)
+// (warpstate/model.py:26-27). One wave per row; the row sum is a wave-level butterfly
+// reduction (__shfl_xor lowers to DPP / ds_swizzle lane exchanges).
+static __global__ void __launch_bounds__(256) rms_rstd_kernel(const unsigned short* __restrict__ x,
+                                                       long ldx, float* __restrict__ rstd,
+                                                       int rows, int D, float eps, int vec) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const unsigned short* xr = x + (long)row * ldx;
+  float acc = 0.0f;
+  if (vec) {
+    for (int c = lane * 8; c < D; c += 64 * 8) {
+      u32x4_t v = *reinterpret_cast<const u32x4_t*>(xr + c);
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        float a = lo_bf16(v[d]), b = hi_bf16(v[d]);
+        acc += a * a;
+        acc += b * b;
+      }
+    }
+  } else {
+    for (int c = lane; c < D; c += 64) {
+      float a = bf16_bits_to_f32(xr[c]);
+      acc += a * a;
+    }
+  }
+  acc = wave_sum(acc);
+  if (lane == 0) rstd[row] = 1.0f / sqrtf(acc / (float)D + eps);
+}
+
+// Standalone BF16 RMSNorm forward (ops/activation_execution.py:96-110): z = x * rstd,
+// y = z * w with z and w rounded to BF16 when eager; also stores rstd.
+static __global__ void __launch_bounds__(256) rmsnorm_fwd_kernel(const unsigned short* __restrict__ x,
+                                                          const float* __restrict__ w,
+                                                          unsigned short* __restrict__ y,
+                                                          float* __restrict__ rstd, int rows,
+                                                          int D, float eps, int eager) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const unsigned short* xr = x + (long)row * D;
+  float acc = 0.0f;
+  for (int c = lane; c < D; c += 64) {
+    float a = bf16_bits_to_f32(xr[c]);
+    acc += a * a;
+  }
+  acc = wave_sum(acc);
+  const float r = 1.0f / sqrtf(acc / (float)D + eps);
+  for (int c = lane; c < D; c += 64) {
+    float z = bf16_bits_to_f32(xr[c]) * r;
+    float wc = w[c];
+    if (eager) {
+      z = rbf16(z);
+      wc = rbf16(wc);
+    }
+    y[(long)row * D + c] = to_bf16_bits(z * wc);
+  }
+  if (lane == 0) rstd[row] = r;
+}
+
+// RMSNorm backward (ops/activation_execution.py:113-141): per row
+//   z = x r, dz = dy w (both BF16-rounded when eager), dr = sum(dz x),
+//   dx = dz r + (-0.5 dr r^3 / D) * 2x; per-group partial weight gradient sum(dy z).
+// One wave per row, `rows_per_block` rows per block write one partial row each.
+static __global__ void __launch_bounds__(256) rmsnorm_bwd_kernel(
+    const unsigned short* __restrict__ x, const float* __restrict__ w,
+    const float* __restrict__ rstd, const unsigned short* __restrict__ dy,
+    unsigned short* __restrict__ dx, float* __restrict__ dw_part, int rows, int D, int eager) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int row = blockIdx.x * 4 + wave;
+  const bool live = row < rows;
+  const float r = live ? rstd[row] : 0.0f;
+  float dr = 0.0f;
+  if (live) {
+    for (int c = lane; c < D; c += 64) {
+      float xv = bf16_bits_to_f32(x[(long)row * D + c]);
+      float wc = w[c];
+      if (eager) wc = rbf16(wc);
+      float dz = bf16_bits_to_f32(dy[(long)row * D + c]) * wc;
+      if (eager) dz = rbf16(dz);
+      dr += dz * xv;
+    }
+  }
+  dr = wave_sum(dr);
+  const float dsq = (-0.5f * dr * (r * r * r)) / (float)D;
+  if (live) {
+    for (int c = lane; c < D; c += 64) {
+      float xv = bf16_bits_to_f32(x[(long)row * D + c]);
+      float wc = w[c];
+      if (eager) wc = rbf16(wc);
+      float dz = bf16_bits_to_f32(dy[(long)row * D + c]) * wc;
+      if (eager) dz = rbf16(dz);
+      dx[(long)row * D + c] = to_bf16_bits(dz * r + dsq * (2.0f * xv));
+    }
+  }
+  // Weight-gradient partial for this block's 4 rows, in row order.
+  extern __shared__ float part[];  // [4][D]
+  for (int c = lane; c < D; c += 64) {
+    float v = 0.0f;
+    if (live) {
+      float z = bf16_bits_to_f32(x[(long)row * D + c]) * r;
+      if (eager) z = rbf16(z);
+      v = bf16_bits_to_f32(dy[(long)row * D + c]) * z;
+      if (eager) v = rbf16(v);
+    }
+    part[wave * D + c] = v;
+  }
+  __syncthreads();
+  for (int c = threadIdx.x; c < D; c += blockDim.x) {
+    dw_part[(long)blockIdx.x * D + c] = ((part[c] + part[D + c]) + part[2 * D + c]) + part[3 * D + c];
+  }
+}
+
+// Column sum of the weight-gradient partials (ops/activation_execution.py:144-158).
+static __global__ void __launch_bounds__(256) rms_weight_reduce_kernel(const float* __restrict__ part,
+                                                                float* __restrict__ dw, int groups,
+                                                                int D, int eager) {
+  const int c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= D) return;
+  float total = 0.0f;
+  for (int gidx = 0; gidx < groups; ++gidx) total += part[(long)gidx * D + c];
+  if (eager) total = rbf16(total);
+  dw[c] = total;
+}
+
+// ---------------------------------------------------------------------------------------
+// Standalone SwiGLU forward over a packed [rows, 2H] projection
+// (ops/activation_execution.py:22-33): out = r?(silu(gate)) * up.
+static __global__ void __launch_bounds__(256) swiglu_fwd_kernel(const unsigned short* __restrict__ packed,
+                                                         unsigned short* __restrict__ out,
+                                                         long total, int H, int eager) {
+  long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  long row = i / H, col = i % H;
+  long p = row * 2 * H + col;
+  float up = bf16_bits_to_f32(packed[p]);
+  float gate = bf16_bits_to_f32(packed[p + H]);
+  float s = silu(gate);
+  if (eager) s = rbf16(s);
+  out[i] = to_bf16_bits(s * up);
+}
+
+// Standalone SwiGLU backward (ops/activation_execution.py:36-55).
+static __global__ void __launch_bounds__(256) swiglu_bwd_kernel(const unsigned short* __restrict__ packed,
+                                                         const unsigned short* __restrict__ dyv,
+                                                         unsigned short* __restrict__ dx,
+                                                         long total, int H, int eager) {
+  long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  long row = i / H, col = i % H;
+  long p = row * 2 * H + col;
+  float up = bf16_bits_to_f32(packed[p]);
+  float gate = bf16_bits_to_f32(packed[p + H]);
+  float dy = bf16_bits_to_f32(dyv[i]);
+  float sg = sigmoid(gate);
+  float s = silu(gate);
+  if (eager) s = rbf16(s);
+  float dsilu = dy * up;
+  if (eager) dsilu = rbf16(dsilu);
+  float dgate = (dsilu * sg) * (1.0f + gate * (1.0f - sg));
+  dx[p] = to_bf16_bits(dy * s);
+  dx[p + H] = to_bf16_bits(dgate);
+}
+
+// ---------------------------------------------------------------------------------------
+// Cross-entropy, pass 1 combine: lse[r] = M + log(sum_p s_p e^(m_p - M)) over the
+// per-(row, column block) partials; loss[r] = lse - logit[target] for targets != -100,
+// else 0 (F.cross_entropy(..., ignore_index=-100, reduction="none") semantics); NaN for a
+// target outside [0, vocab) that is not -100.
+static __global__ void __launch_bounds__(256) ce_combine_kernel(const float* __restrict__ part_max,
+                                                         const float* __restrict__ part_sum,
+                                                         int parts, const float* __restrict__ tgt_logit,
+                                                         const long* __restrict__ targets,
+                                                         float* __restrict__ lse,
+                                                         float* __restrict__ loss, int rows,
+                                                         int vocab) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  float mx = -INFINITY;
+  for (int q = lane; q < parts; q += 64) mx = fmaxf(mx, part_max[(long)row * parts + q]);
+  mx = wave_max(mx);
+  float s = 0.0f;
+  for (int q = lane; q < parts; q += 64) {
+    float pm = part_max[(long)row * parts + q];
+    s += part_sum[(long)row * parts + q] * exp_e(pm - mx);
+  }
+  s = wave_sum(s);
+  if (lane == 0) {
+    float l = mx + log_e(s);
+    lse[row] = l;
+    long t = targets[row];
+    // A target outside [0, vocab) that is not -100 has no logit: report NaN.
+    loss[row] = (t == -100) ? 0.0f : (t < 0 || t >= vocab) ? __builtin_nanf("") : l - tgt_logit[row];
+  }
+}
+
+// Mean over valid tokens, sum(loss) / max(1, count(target != -100)) (warpstate/model.py:334,
+// ops/loss_experiment.py:18-19). One block; a fixed reduction order makes it deterministic.
+// Also writes the backward scale dmean / max(1, count) when dmean is given.
+static __global__ void __launch_bounds__(1024) ce_mean_kernel(const float* __restrict__ loss,
+                                                       const long* __restrict__ targets, int rows,
+                                                       float* __restrict__ mean,
+                                                       float* __restrict__ count_out) {
+  __shared__ float ssum[1024];
+  __shared__ float scnt[1024];
+  float s = 0.0f, c = 0.0f;
+  for (int i = threadIdx.x; i < rows; i += 1024) {
+    s += loss[i];
+    c += targets[i] != -100 ? 1.0f : 0.0f;
+  }
+  ssum[threadIdx.x] = s;
+  scnt[threadIdx.x] = c;
+  __syncthreads();
+  for (int stride = 512; stride > 0; stride >>= 1) {
+    if (threadIdx.x < stride) {
+      ssum[threadIdx.x] += ssum[threadIdx.x + stride];
+      scnt[threadIdx.x] += scnt[threadIdx.x + stride];
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    float cnt = scnt[0];
+    mean[0] = ssum[0] / fmaxf(cnt, 1.0f);
+    count_out[0] = cnt;
+  }
+}
+
+// Backward scale of the summed cross-entropy: dmean / max(1, count).
+static __global__ void ce_scale_kernel(const float* __restrict__ dmean, const float* __restrict__ count,
+                                float* __restrict__ scale) {
+  if (threadIdx.x == 0) scale[0] = dmean[0] / fmaxf(count[0], 1.0f);
+}
+
+// ---------------------------------------------------------------------------------------
+// Split-K reductions. Partials are [splits][M][ld] FP32 slices of one GEMM output.
+// G[m, n] += f32(r(sum_s P_s)) (round) or G += sum_s P_s.
+static __global__ void __launch_bounds__(256) splitk_accum_kernel(const float* __restrict__ part,
+                                                           int splits, long split_stride,
+                                                           float* __restrict__ g, long ldg, int M,
+                                                           int N, int round_acc) {
+  long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  long total = (long)M * N;
+  if (i >= total) return;
+  long m = i / N, n = i % N;
+  float s = 0.0f;
+  for (int q = 0; q < splits; ++q) s += part[q * split_stride + m * N + n];
+  g[m * ldg + n] += round_acc ? rbf16(s) : s;
+}
+
+// out[m, n] = r(sum_s P_s) as BF16.
+static __global__ void __launch_bounds__(256) splitk_bf16_kernel(const float* __restrict__ part,
+                                                          int splits, long split_stride,
+                                                          unsigned short* __restrict__ out,
+                                                          long ldo, int M, int N) {
+  long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  long total = (long)M * N;
+  if (i >= total) return;
+  long m = i / N, n = i % N;
+  float s = 0.0f;
+  for (int q = 0; q < splits; ++q) s += part[q * split_stride + m * N + n];
+  out[m * ldo + n] = to_bf16_bits(s);
+}
+
+}  // namespace ws

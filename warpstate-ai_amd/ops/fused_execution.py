@@ -1,0 +1,244 @@
+"""Fused BF16 GEMMs of the WarpState training step on gfx950 (additive entry points).
+
+The reference composes these from separate operators; here each is one GEMM launch whose
+prologue or epilogue does the extra work in registers:
+
+* ``rmsnorm_gate_mm``: RMSNorm (warpstate/model.py:22-28) as the prologue of the fused
+  input projection (warpstate/model.py:93,109), with sigmoid on the gate column range
+  (warpstate/model.py:174). A row-statistics pass (one read of x) precedes the GEMM; the
+  normalized operand is formed while the A tile is staged and never stored.
+* ``residual_mm``: down projection plus the BF16 residual add (warpstate/model.py:178,
+  ops/residual_experiment.py:25-58).
+* ``swiglu_backward_mm``: the down projection's input gradient (ops/matmul_execution.py:239)
+  with the SwiGLU backward (ops/activation_execution.py:36-55) as its epilogue.
+* ``mm_accumulate_``: weight-gradient GEMM accumulated into an FP32 buffer,
+  G += f32(r(dW)) (test_gradient_execution.py:243-246).
+* ``linear_cross_entropy_*``: the tied LM head with fused cross-entropy
+  (warpstate/model.py:316-334, ops/loss_experiment.py:14-19); logits never reach HBM.
+* ``mlp_backward``: the SwiGLU MLP backward at training shape built from the above.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from ops import _hip
+
+DEFAULT_CE_CHUNK_ROWS = 2048
+
+
+def _check_bf16_cuda(*tensors):
+    for tensor in tensors:
+        if not tensor.is_cuda:
+            raise ValueError("Fused matrix kernels require CUDA tensors")
+        if tensor.dtype != torch.bfloat16:
+            raise ValueError("Fused matrix kernels require BF16 operands")
+
+
+def mm(a: torch.Tensor, b: torch.Tensor, algorithm: str = "tiled", tile: int = 0) -> torch.Tensor:
+    """r(a @ b) with the HIP GEMM; `tile` 0 = 256x256, 1 = 128x128."""
+    _check_bf16_cuda(a, b)
+    m, k = a.shape
+    n = b.shape[1]
+    out = torch.empty((m, n), dtype=torch.bfloat16, device=a.device)
+    _hip.call("ws_mm", a.data_ptr(), a.stride(0), a.stride(1), b.data_ptr(), b.stride(0),
+              b.stride(1), out.data_ptr(), m, n, k, _hip.algorithm_code(algorithm), tile,
+              _hip.stream(a))
+    return out
+
+
+def rmsnorm_gate_mm(x: torch.Tensor, norm_weight: torch.Tensor, eps: float,
+                    weight: torch.Tensor, gate: tuple[int, int] = (0, 0),
+                    out: torch.Tensor | None = None, rstd: torch.Tensor | None = None
+                    ) -> tuple[torch.Tensor, torch.Tensor]:
+    """``(r(RMSNorm(x) @ weight.T) with sigmoid on columns [gate), rstd)``.
+
+    x [M, K] BF16 with unit column stride; norm_weight [K] FP32; weight [N, K] BF16 in
+    nn.Linear layout; gate = (begin, end) output columns that get r(sigmoid(.)).
+    """
+    _check_bf16_cuda(x, weight)
+    if x.ndim != 2 or weight.ndim != 2 or x.shape[1] != weight.shape[1]:
+        raise ValueError("Expected x [M, K] and weight [N, K]")
+    if x.stride(1) != 1:
+        raise ValueError("The RMSNorm prologue needs a unit column stride")
+    if norm_weight.dtype != torch.float32 or not norm_weight.is_contiguous():
+        raise ValueError("RMSNorm weight must be a contiguous FP32 vector")
+    m, k = x.shape
+    n = weight.shape[0]
+    if out is None:
+        out = torch.empty((m, n), dtype=torch.bfloat16, device=x.device)
+    if rstd is None:
+        rstd = torch.empty((m,), dtype=torch.float32, device=x.device)
+    b = weight.T
+    _hip.call("ws_rmsnorm_gate_mm", x.data_ptr(), x.stride(0), norm_weight.data_ptr(),
+              float(eps), rstd.data_ptr(), b.data_ptr(), b.stride(0), b.stride(1),
+              out.data_ptr(), m, n, k, int(gate[0]), int(gate[1]), _hip.stream(x))
+    return out, rstd
+
+
+def residual_mm(a: torch.Tensor, weight: torch.Tensor, residual: torch.Tensor,
+                out: torch.Tensor | None = None) -> torch.Tensor:
+    """r(residual + r(a @ weight.T)); a [M, K], weight [N, K], residual [M, N] (unit
+    column stride)."""
+    _check_bf16_cuda(a, weight, residual)
+    m, k = a.shape
+    n = weight.shape[0]
+    if weight.shape[1] != k or residual.shape != (m, n) or residual.stride(1) != 1:
+        raise ValueError("Expected a [M, K], weight [N, K] and a row-major residual [M, N]")
+    if out is None:
+        out = torch.empty((m, n), dtype=torch.bfloat16, device=a.device)
+    b = weight.T
+    _hip.call("ws_residual_mm", a.data_ptr(), a.stride(0), a.stride(1), b.data_ptr(),
+              b.stride(0), b.stride(1), residual.data_ptr(), residual.stride(0),
+              out.data_ptr(), m, n, k, _hip.stream(a))
+    return out
+
+
+def swiglu_backward_mm(grad: torch.Tensor, down_weight: torch.Tensor, packed: torch.Tensor,
+                       eager_rounding: bool = True,
+                       out: torch.Tensor | None = None) -> torch.Tensor:
+    """dPacked [M, 2H] from dY [M, d], the down weight [d, H] (nn.Linear layout) and the
+    saved packed projection [M, 2H] (contiguous)."""
+    _check_bf16_cuda(grad, down_weight, packed)
+    m, k = grad.shape
+    h = down_weight.shape[1]
+    if down_weight.shape[0] != k or packed.shape != (m, 2 * h) or not packed.is_contiguous():
+        raise ValueError("Expected dY [M, d], down weight [d, H], contiguous packed [M, 2H]")
+    if out is None:
+        out = torch.empty((m, 2 * h), dtype=torch.bfloat16, device=grad.device)
+    _hip.call("ws_swiglu_backward_mm", grad.data_ptr(), grad.stride(0), grad.stride(1),
+              down_weight.data_ptr(), down_weight.stride(0), down_weight.stride(1),
+              packed.data_ptr(), out.data_ptr(), m, h, k, int(eager_rounding), _hip.stream(grad))
+    return out
+
+
+def mm_accumulate_(g: torch.Tensor, a: torch.Tensor, b: torch.Tensor, round_bf16: bool = True,
+                   splits: int = 1, workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """G += f32(r(a @ b)) (or G += a @ b in FP32 when ``round_bf16`` is False), in place.
+
+    G is FP32 [M, N] with unit column stride; ``splits`` > 1 splits the reduction through
+    an FP32 workspace of splits * M * N floats."""
+    _check_bf16_cuda(a, b)
+    if g.dtype != torch.float32 or g.stride(1) != 1:
+        raise ValueError("Gradient buffer must be FP32 with unit column stride")
+    m, k = a.shape
+    n = b.shape[1]
+    if g.shape != (m, n) or b.shape[0] != k:
+        raise ValueError("Gradient buffer shape must match a @ b")
+    need = _hip.query("ws_mm_accumulate_workspace_floats", m, n, splits)
+    if need and (workspace is None or workspace.numel() < need):
+        workspace = torch.empty((need,), dtype=torch.float32, device=g.device)
+    _hip.call("ws_mm_accumulate_f32", a.data_ptr(), a.stride(0), a.stride(1), b.data_ptr(),
+              b.stride(0), b.stride(1), g.data_ptr(), g.stride(0), m, n, k, int(round_bf16),
+              None if not need else workspace.data_ptr(), splits, _hip.stream(a))
+    return g
+
+
+class CrossEntropyState:
+    """Per-call buffers of the fused LM-head cross-entropy."""
+
+    def __init__(self, rows, vocab, device, chunk_rows=DEFAULT_CE_CHUNK_ROWS):
+        parts = _hip.query("ws_linear_ce_parts", vocab)
+        f32 = dict(dtype=torch.float32, device=device)
+        self.part_max = torch.empty((rows, parts), **f32)
+        self.part_sum = torch.empty((rows, parts), **f32)
+        self.target_logit = torch.empty((rows,), **f32)
+        self.lse = torch.empty((rows,), **f32)
+        self.loss = torch.empty((rows,), **f32)
+        self.mean = torch.empty((), **f32)
+        self.count = torch.empty((), **f32)
+        self.scale = torch.empty((1,), **f32)
+        self.chunk_rows = min(chunk_rows, rows)
+        self.grad_logits = torch.empty((self.chunk_rows, vocab), dtype=torch.bfloat16,
+                                       device=device)
+
+
+def _check_ce(hidden, weight, targets):
+    _check_bf16_cuda(hidden, weight)
+    if hidden.ndim != 2 or weight.ndim != 2 or hidden.shape[1] != weight.shape[1]:
+        raise ValueError("Expected hidden [rows, d] and weight [vocab, d]")
+    if hidden.stride(1) != 1 or weight.stride(1) != 1:
+        raise ValueError("LM-head operands need a unit column stride")
+    if targets.dtype != torch.int64 or targets.shape != (hidden.shape[0],) or not targets.is_contiguous():
+        raise ValueError("Targets must be a contiguous int64 vector, one per row")
+
+
+def linear_cross_entropy_forward(hidden: torch.Tensor, weight: torch.Tensor,
+                                 targets: torch.Tensor, state: CrossEntropyState | None = None
+                                 ) -> CrossEntropyState:
+    """Per-token loss, lse, mean over valid tokens and their count, for hidden [rows, d],
+    weight [vocab, d] and int64 targets (-100 ignored)."""
+    _check_ce(hidden, weight, targets)
+    rows, d = hidden.shape
+    vocab = weight.shape[0]
+    if state is None:
+        state = CrossEntropyState(rows, vocab, hidden.device)
+    _hip.call("ws_linear_ce_forward", hidden.data_ptr(), hidden.stride(0), weight.data_ptr(),
+              weight.stride(0), targets.data_ptr(), rows, vocab, d, state.part_max.data_ptr(),
+              state.part_sum.data_ptr(), state.target_logit.data_ptr(), state.lse.data_ptr(),
+              state.loss.data_ptr(), state.mean.data_ptr(), state.count.data_ptr(),
+              _hip.stream(hidden))
+    return state
+
+
+def linear_cross_entropy_backward(hidden: torch.Tensor, weight: torch.Tensor,
+                                  targets: torch.Tensor, state: CrossEntropyState,
+                                  grad_mean: torch.Tensor,
+                                  out: torch.Tensor | None = None) -> torch.Tensor:
+    """dHidden [rows, d] BF16 of ``mean`` given its FP32 scalar gradient."""
+    _check_ce(hidden, weight, targets)
+    rows, d = hidden.shape
+    vocab = weight.shape[0]
+    grad_mean = grad_mean.reshape(1).to(torch.float32).contiguous()
+    if out is None:
+        out = torch.empty((rows, d), dtype=torch.bfloat16, device=hidden.device)
+    _hip.call("ws_linear_ce_backward", hidden.data_ptr(), hidden.stride(0), weight.data_ptr(),
+              weight.stride(0), targets.data_ptr(), state.lse.data_ptr(), state.count.data_ptr(),
+              grad_mean.data_ptr(), rows, vocab, d, state.grad_logits.data_ptr(),
+              state.chunk_rows, state.scale.data_ptr(), out.data_ptr(), out.stride(0),
+              _hip.stream(hidden))
+    return out
+
+
+class LinearCrossEntropy(torch.autograd.Function):
+    """mean cross-entropy of r(hidden @ weight.T) with the gradient to ``hidden``.
+
+    The tied weight receives no gradient from this function."""
+
+    @staticmethod
+    def forward(ctx, hidden, weight, targets):
+        state = linear_cross_entropy_forward(hidden, weight, targets)
+        ctx.save_for_backward(hidden, weight, targets)
+        ctx.state = state
+        ctx.mark_non_differentiable(state.loss)
+        return state.mean.clone(), state.loss
+
+    @staticmethod
+    def backward(ctx, grad_mean, _grad_loss):
+        hidden, weight, targets = ctx.saved_tensors
+        dhidden = linear_cross_entropy_backward(hidden, weight, targets, ctx.state, grad_mean)
+        return dhidden, None, None
+
+
+def linear_cross_entropy(hidden, weight, targets):
+    """(mean, per-token loss) with autograd to ``hidden``."""
+    return LinearCrossEntropy.apply(hidden, weight, targets)
+
+
+def mlp_backward(x: torch.Tensor, w_upgate: torch.Tensor, w_down: torch.Tensor,
+                 packed: torch.Tensor, act: torch.Tensor, dy: torch.Tensor,
+                 g_upgate: torch.Tensor, g_down: torch.Tensor, eager_rounding: bool = True,
+                 dw_splits: int = 1) -> torch.Tensor:
+    """Backward of y = down(silu(gate) * up) with (up | gate) = x @ w_upgate.T.
+
+    x [M, d], w_upgate [2H, d], w_down [d, H] (nn.Linear layouts, BF16), packed [M, 2H] and
+    act [M, H] saved from the forward, dy [M, d]. Accumulates G_down [d, H] += f32(r(dY^T act))
+    and G_upgate [2H, d] += f32(r(dPacked^T x)); returns dX [M, d]. Restates
+    ops/matmul_execution.py:236-244 and :314-319 with the SwiGLU backward fused on the
+    dAct GEMM.
+    """
+    dpacked = swiglu_backward_mm(dy, w_down, packed, eager_rounding)
+    dx = mm(dpacked, w_upgate)
+    mm_accumulate_(g_down, dy.T, act, True, dw_splits)
+    mm_accumulate_(g_upgate, dpacked.T, x, True, dw_splits)
+    return dx

@@ -1,0 +1,97 @@
+"""Module types of the hot path and a small LM built from them (see package docstring).
+
+RMSNorm, SwiGLU, the residual adds and the chunked tied-head loss follow the numerics of
+warpstate/model.py:15-28, :52-60, :177-178 and :316-334; the token mixer between
+``in_proj`` and ``out_proj`` is a placeholder.
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+from torch.utils.checkpoint import checkpoint
+
+from .config import WarpStateConfig
+
+
+class RMSNorm(nn.Module):
+    def __init__(self, dim: int, eps: float = 1e-5):
+        super().__init__()
+        self.weight = nn.Parameter(torch.ones(dim))
+        self.eps = eps
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        # FP32 statistics, BF16-rounded normalized value times the cast weight.
+        wide = x.float()
+        wide = wide * torch.rsqrt(wide.pow(2).mean(dim=-1, keepdim=True) + self.eps)
+        return wide.to(x.dtype) * self.weight.to(x.dtype)
+
+
+class SwiGLU(nn.Module):
+    """Packed projection: up in output columns [0, hidden), gate in [hidden, 2 hidden)."""
+
+    def __init__(self, dim: int, hidden: int):
+        super().__init__()
+        self.up_gate = nn.Linear(dim, hidden * 2, bias=False)
+        self.down = nn.Linear(hidden, dim, bias=False)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        up, gate = self.up_gate(x).chunk(2, dim=-1)
+        return self.down(F.silu(gate) * up)
+
+
+class WarpStateCore(nn.Module):
+    def __init__(self, cfg: WarpStateConfig):
+        super().__init__()
+        d = cfg.d_model
+        self.norm1 = RMSNorm(d, cfg.rms_eps)
+        self.in_proj = nn.Linear(d, 5 * d, bias=False)
+        self.out_proj = nn.Linear(d, d, bias=False)
+        self.norm2 = RMSNorm(d, cfg.rms_eps)
+        self.ffn = SwiGLU(d, cfg.ffn_hidden)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        q, k, v, g, u = self.in_proj(self.norm1(x)).chunk(5, dim=-1)
+        gate = torch.sigmoid(g)
+        mixed = gate * v + (1 - gate) * torch.tanh(q * k + u)
+        x = x + self.out_proj(mixed)
+        return x + self.ffn(self.norm2(x))
+
+
+class WarpStateLM(nn.Module):
+    def __init__(self, cfg: WarpStateConfig):
+        super().__init__()
+        cfg.validate()
+        self.cfg = cfg
+        self.embed = nn.Embedding(cfg.vocab_size, cfg.d_model)
+        self.cores = nn.ModuleList([WarpStateCore(cfg) for _ in range(cfg.n_cores)])
+        self.depth_scale = nn.Parameter(torch.zeros(cfg.logical_depth, cfg.d_model))
+        self.depth_bias = nn.Parameter(torch.zeros(cfg.logical_depth, cfg.d_model))
+        self.final_norm = RMSNorm(cfg.d_model, cfg.rms_eps)
+        for module in self.modules():
+            if isinstance(module, (nn.Linear, nn.Embedding)):
+                nn.init.normal_(module.weight, mean=0.0, std=0.02)
+
+    def forward(self, input_ids, targets=None, *, return_logits=True):
+        x = self.embed(input_ids)
+        for depth in range(self.cfg.logical_depth):
+            x = x * (1.0 + self.depth_scale[depth]) + self.depth_bias[depth]
+            core = self.cores[depth % self.cfg.n_cores]
+            if self.training and self.cfg.gradient_checkpointing:
+                x = checkpoint(core, x, use_reentrant=False)
+            else:
+                x = core(x)
+        x = self.final_norm(x)
+        if targets is not None and not return_logits:
+            hidden = x.reshape(-1, x.size(-1))
+            labels = targets.reshape(-1)
+            loss = x.new_zeros((), dtype=torch.float32)
+            step = self.cfg.loss_chunk_size
+            for start in range(0, labels.numel(), step):
+                logits = F.linear(hidden[start:start + step], self.embed.weight).float()
+                loss = loss + F.cross_entropy(logits, labels[start:start + step], reduction="sum")
+            return None, loss / labels.ne(-100).sum().clamp_min(1)
+        logits = F.linear(x, self.embed.weight)
+        if targets is None:
+            return logits
+        return logits, F.cross_entropy(logits.reshape(-1, logits.size(-1)), targets.reshape(-1))
