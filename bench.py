@@ -1,0 +1,350 @@
+"""Benchmark of the fused BF16 GEMM hot path on one MI355X.
+
+One step is one pass of the hot path of a WarpState layer at training shape, M = 16384
+tokens (batch 8 x seq 2048), d = 2048, ffn = 5632, on synthetic seeded inputs resident in
+HBM:
+
+  qkv_fwd      RMSNorm-prologue fused projection [16384,2048] x [2048,9216], sigmoid on
+               the gate slice                                                 (config 2)
+  swiglu_fwd   paired up/gate GEMM [16384,2048] x [2048,11264] with SwiGLU epilogue
+  down_fwd     down projection [16384,5632] x [5632,2048] with residual add  (config 3)
+  mlp_bwd      SwiGLU MLP backward: dH with fused SwiGLU backward, dX, and FP32-
+               accumulated wgrad of W_down and W_upgate                      (config 4)
+  qkv_bwd      input-projection dX [16384,9216] x [9216,2048] and FP32-accumulated
+               wgrad [9216,16384] x [16384,2048]
+
+``value`` is the step's algorithmic FLOPs over its wall time (TFLOP/s). The other two
+configurations are timed beside it and reported under ``per_config``: config 1 (SwiGLU
+4096 x 1024 -> 2 x 2816) and config 5 (LM head with fused cross-entropy, forward
+statistics + dHidden, 16384 x 2048 -> 32768, logits never in HBM).
+
+``roofline`` describes the dominant kernel of the step (the FP32-accumulating wgrad GEMM
+of the MLP backward by default); its average launch time comes from HIP events around
+each launch on the stream it runs on. ``cpu_baseline`` times the CPU oracle (the
+reference's eager PyTorch path restated) on a row sample of the same step.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _path in (ROOT, ROOT / "warpstate-ai_amd"):
+    if str(_path) not in sys.path:
+        sys.path.insert(0, str(_path))
+
+import torch  # noqa: E402
+
+PEAK_BF16_TFLOPS = 2516.6  # 256 CU x 4096 dense BF16 FLOP/clk/CU x 2.4 GHz
+PEAK_HBM_GBS = 8000.0
+METRIC = "fused-epilogue BF16 GEMM TFLOP/s + % MFMA peak, M=16384 SwiGLU/QKV fwd+bwd"
+
+M, D, FFN, NQKV, VOCAB = 16384, 2048, 5632, 9216, 32768
+GATE = (6144, 8192)
+
+
+def parse():
+    p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--rows", type=int, default=M, help="tokens per step (default 16384)")
+    p.add_argument("--cpu-rows", type=int, default=2048,
+                   help="row sample of the CPU-baseline step")
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    p.add_argument("--no-extra", action="store_true", help="skip configs 1 and 5")
+    return p.parse_args()
+
+
+def flops_step(m):
+    qkv = 2 * m * D * NQKV
+    swiglu = 2 * m * D * 2 * FFN
+    down = 2 * m * FFN * D
+    mlp_bwd = 2 * m * D * FFN + 2 * m * 2 * FFN * D + 2 * D * FFN * m + 2 * 2 * FFN * D * m
+    qkv_bwd = 2 * m * NQKV * D + 2 * NQKV * m * D
+    return {"qkv_fwd": qkv, "swiglu_fwd": swiglu, "down_fwd": down, "mlp_bwd": mlp_bwd,
+            "qkv_bwd": qkv_bwd}
+
+
+class Timer:
+    """HIP-event timing of named regions on the current stream."""
+
+    def __init__(self):
+        self.events = {}
+
+    def region(self, name):
+        timer = self
+
+        class _Region:
+            def __enter__(self):
+                self.start = torch.cuda.Event(enable_timing=True)
+                self.end = torch.cuda.Event(enable_timing=True)
+                self.start.record()
+
+            def __exit__(self, *exc):
+                self.end.record()
+                timer.events.setdefault(name, []).append((self.start, self.end))
+
+        return _Region()
+
+    def mean_ms(self, name):
+        pairs = self.events.get(name, [])
+        return sum(s.elapsed_time(e) for s, e in pairs) / max(1, len(pairs))
+
+    def reset(self):
+        self.events = {}
+
+
+def gpu_inputs(m, device):
+    from ops.benchmark_configs import (down_residual_inputs, mlp_backward_inputs,
+                                       rms_projection_inputs)
+
+    qkv = rms_projection_inputs(m=m, d=D, n=NQKV, gate=GATE, seed=0)
+    down = down_residual_inputs(m=m, ffn=FFN, d=D, seed=0)
+    mlp = mlp_backward_inputs(m=m, d=D, ffn=FFN, seed=0)
+    dev = {}
+    for prefix, group in (("qkv", qkv), ("down", down), ("mlp", mlp)):
+        for key, value in group.items():
+            dev[f"{prefix}_{key}"] = value.to(device) if torch.is_tensor(value) else value
+    # Upstream gradient of the input projection (bf16 ~N(0, 1e-2)) and its FP32 wgrad buffer.
+    gen = torch.Generator("cpu").manual_seed(1)
+    dev["qkv_dp"] = (torch.randn((m, NQKV), generator=gen) * 1e-2).bfloat16().to(device)
+    dev["qkv_g"] = (torch.randn((NQKV, D), generator=gen) * 1e-4).to(device)
+    return dev
+
+
+def run_step(inp, out, timer=None):
+    """One hot-path pass; every kernel launches through the C ABI on the current stream."""
+    from contextlib import nullcontext
+
+    from ops.fused_execution import (mm, mm_accumulate_, residual_mm, rmsnorm_gate_mm,
+                                     swiglu_backward_mm)
+    from ops.matmul_epilogue import launch_swiglu_mm
+
+    reg = timer.region if timer else (lambda name: nullcontext())
+    with reg("qkv_fwd"):
+        rmsnorm_gate_mm(inp["qkv_x"], inp["qkv_norm_weight"], inp["qkv_eps"], inp["qkv_w"],
+                        GATE, out=out["qkv"], rstd=out["rstd"])
+    with reg("swiglu_fwd"):
+        packed, act = launch_swiglu_mm(inp["mlp_x"], inp["mlp_w_upgate"].T, "tiled",
+                                       (128, 128, 32, 8, 3), True)
+    with reg("down_fwd"):
+        residual_mm(inp["down_h"], inp["down_w_down"], inp["down_residual"], out=out["down"])
+    with reg("mlp_bwd"):
+        with reg("mlp_bwd.dact_swiglu"):
+            dpacked = swiglu_backward_mm(inp["mlp_dy"], inp["mlp_w_down"], packed, True,
+                                         out=out["dpacked"])
+        with reg("mlp_bwd.dx"):
+            mm(dpacked, inp["mlp_w_upgate"])
+        with reg("mlp_bwd.wgrad_down"):
+            mm_accumulate_(inp["mlp_g_down"], inp["mlp_dy"].T, act, True)
+        with reg("mlp_bwd.wgrad_upgate"):
+            mm_accumulate_(inp["mlp_g_upgate"], dpacked.T, inp["mlp_x"], True)
+    with reg("qkv_bwd"):
+        with reg("qkv_bwd.dx"):
+            mm(inp["qkv_dp"], inp["qkv_w"])
+        with reg("qkv_bwd.wgrad"):
+            mm_accumulate_(inp["qkv_g"], inp["qkv_dp"].T, out["qkv_z"], True)
+
+
+def bench_gpu(args):
+    device = torch.device("cuda:0")
+    m = args.rows
+    inp = gpu_inputs(m, device)
+    out = {"qkv": torch.empty((m, NQKV), dtype=torch.bfloat16, device=device),
+           "rstd": torch.empty((m,), dtype=torch.float32, device=device),
+           "down": torch.empty((m, D), dtype=torch.bfloat16, device=device),
+           "dpacked": torch.empty((m, 2 * FFN), dtype=torch.bfloat16, device=device),
+           # The normalized input saved for the wgrad of the input projection.
+           "qkv_z": torch.empty((m, D), dtype=torch.bfloat16, device=device)}
+    from ops.activation_execution import bf16_rmsnorm
+
+    out["qkv_z"].copy_(bf16_rmsnorm(inp["qkv_x"], inp["qkv_norm_weight"], inp["qkv_eps"])[0])
+    for _ in range(args.warmup):
+        run_step(inp, out)
+    torch.cuda.synchronize()
+    # Timed region: exactly `steps` steps, synchronised on both sides.
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        run_step(inp, out)
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    # Per-region HIP-event times over separate steps (not part of the timed region).
+    timer = Timer()
+    for _ in range(args.steps):
+        run_step(inp, out, timer)
+    torch.cuda.synchronize()
+    flops = flops_step(m)
+    regions = {}
+    for name, f in flops.items():
+        ms = timer.mean_ms(name)
+        regions[name] = {"ms": round(ms, 4), "tflops": round(f / ms / 1e9, 1),
+                         "pct_peak": round(100 * f / ms / 1e9 / PEAK_BF16_TFLOPS, 2)}
+    sub = {"mlp_bwd.dact_swiglu": 2 * m * D * FFN, "mlp_bwd.dx": 2 * m * 2 * FFN * D,
+           "mlp_bwd.wgrad_down": 2 * D * FFN * m, "mlp_bwd.wgrad_upgate": 2 * 2 * FFN * D * m,
+           "qkv_bwd.dx": 2 * m * NQKV * D, "qkv_bwd.wgrad": 2 * NQKV * m * D}
+    kernels = {}
+    for name, f in sub.items():
+        ms = timer.mean_ms(name)
+        kernels[name] = {"ms": round(ms, 4), "tflops": round(f / ms / 1e9, 1),
+                         "pct_peak": round(100 * f / ms / 1e9 / PEAK_BF16_TFLOPS, 2),
+                         "flops": f}
+    # RMSNorm statistics pass (HBM-bound part of qkv_fwd): one read of x, one rstd write.
+    from ops import _hip
+
+    rt = Timer()
+    for _ in range(args.steps):
+        with rt.region("rstd"):
+            _hip.call("ws_rms_rstd", inp["qkv_x"].data_ptr(), D, out["rstd"].data_ptr(), m, D,
+                      float(inp["qkv_eps"]), _hip.stream(inp["qkv_x"]))
+    torch.cuda.synchronize()
+    rstd_ms = rt.mean_ms("rstd")
+    rstd_bytes = m * D * 2 + m * 4
+    hbm = {"rms_rstd": {"ms": round(rstd_ms, 4), "bytes": rstd_bytes,
+                        "gbs": round(rstd_bytes / rstd_ms / 1e6, 1)}}
+    return wall_ms, sum(flops.values()), regions, kernels, hbm, inp, out
+
+
+def bench_extra(args, device):
+    """Configs 1 and 5, each timed over `steps` launches with HIP events."""
+    from ops.benchmark_configs import lm_head_inputs, swiglu_forward_inputs
+    from ops.fused_execution import (CrossEntropyState, linear_cross_entropy_backward,
+                                     linear_cross_entropy_forward)
+    from ops.matmul_epilogue import launch_swiglu_mm
+
+    res = {}
+    c1 = swiglu_forward_inputs(seed=0)
+    x, w = c1["x"].to(device), c1["w_upgate"].to(device)
+    for _ in range(args.warmup):
+        launch_swiglu_mm(x, w.T, "tiled", (128, 128, 32, 8, 3), True)
+    t = Timer()
+    for _ in range(args.steps):
+        with t.region("c1"):
+            launch_swiglu_mm(x, w.T, "tiled", (128, 128, 32, 8, 3), True)
+    torch.cuda.synchronize()
+    f1 = 2 * 4096 * 1024 * 5632
+    ms = t.mean_ms("c1")
+    res["config1_swiglu_4096x1024x5632"] = {"ms": round(ms, 4), "tflops": round(f1 / ms / 1e9, 1),
+                                            "pct_peak": round(100 * f1 / ms / 1e9 / PEAK_BF16_TFLOPS, 2)}
+    del x, w
+    c5 = lm_head_inputs(seed=0)
+    hidden, weight, targets = (c5[k].to(device) for k in ("hidden", "weight", "targets"))
+    state = CrossEntropyState(M, VOCAB, device)
+    dh = torch.empty((M, D), dtype=torch.bfloat16, device=device)
+    one = torch.ones((), device=device)
+
+    def ce():
+        linear_cross_entropy_forward(hidden, weight, targets, state)
+        linear_cross_entropy_backward(hidden, weight, targets, state, one, out=dh)
+
+    for _ in range(args.warmup):
+        ce()
+    t = Timer()
+    for _ in range(args.steps):
+        with t.region("fwd"):
+            linear_cross_entropy_forward(hidden, weight, targets, state)
+        with t.region("bwd"):
+            linear_cross_entropy_backward(hidden, weight, targets, state, one, out=dh)
+    torch.cuda.synchronize()
+    f5 = 4 * M * D * VOCAB
+    ms = t.mean_ms("fwd") + t.mean_ms("bwd")
+    res["config5_lm_head_ce_16384x2048x32768"] = {
+        "ms": round(ms, 4), "fwd_ms": round(t.mean_ms("fwd"), 4),
+        "bwd_ms": round(t.mean_ms("bwd"), 4), "tflops": round(f5 / ms / 1e9, 1),
+        "pct_peak": round(100 * f5 / ms / 1e9 / PEAK_BF16_TFLOPS, 2),
+        "flops_note": "logits fwd + dHidden; the backward's logit recompute is not counted"}
+    return res
+
+
+def cpu_baseline(rows):
+    """The CPU oracle (the reference's eager PyTorch path restated) on `rows` tokens of the
+    same step; returns (TFLOP/s, seconds per step, threads)."""
+    from oracle import reference as oracle
+    from ops.benchmark_configs import (down_residual_inputs, mlp_backward_inputs,
+                                       rms_projection_inputs)
+
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    qkv = rms_projection_inputs(m=rows, d=D, n=NQKV, gate=GATE, seed=0)
+    down = down_residual_inputs(m=rows, ffn=FFN, d=D, seed=0)
+    mlp = mlp_backward_inputs(m=rows, d=D, ffn=FFN, seed=0)
+    gen = torch.Generator("cpu").manual_seed(1)
+    dp = (torch.randn((rows, NQKV), generator=gen) * 1e-2).bfloat16()
+    g_qkv = torch.randn((NQKV, D), generator=gen) * 1e-4
+    z = oracle.rmsnorm(qkv["x"], qkv["norm_weight"], qkv["eps"])
+
+    def step():
+        oracle.rmsnorm_gate_projection(qkv["x"], qkv["norm_weight"], qkv["eps"], qkv["w"], GATE)
+        packed, act = oracle.swiglu_mm(mlp["x"], mlp["w_upgate"].T, True)
+        oracle.residual_projection(down["h"], down["w_down"], down["residual"])
+        oracle.mlp_backward(mlp["x"], mlp["w_upgate"], mlp["w_down"], packed, act, mlp["dy"],
+                            mlp["g_upgate"], mlp["g_down"])
+        torch.mm(dp, qkv["w"])
+        oracle.accumulate_weight_grad(g_qkv, dp.T, z)
+
+    step()  # warmup
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 3 or (time.perf_counter() - t_start < 10 and len(times) < 20):
+        t0 = time.perf_counter()
+        step()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    sec = times[len(times) // 2]
+    return sum(flops_step(rows).values()) / sec / 1e12, sec, torch.get_num_threads()
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path "
+              "(the hot path shards over tokens; see the design notes). Use --gpus 1.",
+              file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU (MI355X)", file=sys.stderr)
+        sys.exit(2)
+    device = torch.device("cuda:0")
+    wall_ms, step_flops, regions, kernels, hbm, inp, out = bench_gpu(args)
+    del inp, out
+    torch.cuda.empty_cache()
+    per_config = {} if args.no_extra else bench_extra(args, device)
+    value = step_flops / wall_ms / 1e9
+    dom_name = max(kernels, key=lambda k: kernels[k]["ms"])
+    dom = kernels[dom_name]
+    roofline = {"bound": "mfma", "kernel": dom_name,
+                "achieved": round(dom["flops"] / dom["ms"] / 1e9, 1),
+                "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(dom["flops"] / dom["ms"] / 1e9 / PEAK_BF16_TFLOPS, 4),
+                "traffic": None}
+    cpu = None
+    if not args.no_cpu:
+        tflops, sec, threads = cpu_baseline(args.cpu_rows)
+        cpu = {"value": round(tflops, 4), "unit": "TFLOP/s", "cores": threads,
+               "kind": "port",
+               "sample": f"the same step at M={args.cpu_rows} tokens (of {args.rows}), "
+                         f"median of >=3 runs, {sec:.2f} s/step, "
+                         f"CPU '{platform.processor() or platform.machine()}'"}
+    line = {"metric": METRIC, "value": round(value, 1), "unit": "TFLOP/s", "n_gpus": 1,
+            "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(wall_ms, 4),
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+            "data": "synthetic (seeded N(0,s) inputs, random-init weights)",
+            "config": {"workload": "WarpState layer hot path fwd+bwd: RMSNorm-QKV/gate "
+                                   "projection, SwiGLU up/gate, down+residual, MLP backward, "
+                                   "QKV backward",
+                       "tokens": args.rows, "d_model": D, "ffn_hidden": FFN,
+                       "qkv_width": NQKV, "step_gflop": round(step_flops / 1e9, 1)},
+            "pct_peak": round(100 * value / PEAK_BF16_TFLOPS, 2),
+            "roofline": roofline, "cpu_baseline": cpu, "regions": regions,
+            "kernels": kernels, "per_config": per_config, "hbm_parts": hbm}
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()
