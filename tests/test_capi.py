@@ -1,0 +1,60 @@
+"""The C-ABI library loads on a CPU-only host and exports every symbol its header declares.
+
+No compute entry point is called here (there is no GPU); the size queries, which do no
+device work, are checked against their documented formulas.
+"""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from ops import _hip
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADERS = sorted((ROOT / "include").glob("*.h"))
+
+
+def declared_symbols():
+    names = set()
+    for header in HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", header.read_text(), flags=re.S)
+        names.update(re.findall(r"\b(ws_[a-z0-9_]+)\s*\(", text))
+    return names
+
+
+def test_header_declares_the_entry_points():
+    names = declared_symbols()
+    assert {"ws_mm", "ws_swiglu_mm", "ws_rmsnorm_gate_mm", "ws_residual_mm",
+            "ws_swiglu_backward_mm", "ws_mm_accumulate_f32", "ws_linear_ce_forward",
+            "ws_linear_ce_backward", "ws_last_error"} <= names
+
+
+def test_library_exports_every_declared_symbol_and_binding_matches():
+    if not _hip.LIBRARY_PATH.exists():
+        pytest.fail(f"{_hip.LIBRARY_PATH} missing: run __graft_entry__.build()")
+    lib = ctypes.CDLL(str(_hip.LIBRARY_PATH))
+    names = declared_symbols()
+    missing = [n for n in sorted(names) if not hasattr(lib, n)]
+    assert not missing, missing
+    # The ctypes signature table covers exactly the declared entry points.
+    assert set(_hip.SIGNATURES) == names
+
+
+def test_queries_without_device_work():
+    lib = _hip.library()
+    assert lib.ws_version().startswith(b"warpstate-hip")
+    assert _hip.query("ws_linear_ce_parts", 32768) == 2 * 128
+    assert _hip.query("ws_mm_accumulate_workspace_floats", 10, 20, 1) == 0
+    assert _hip.query("ws_mm_accumulate_workspace_floats", 10, 20, 4) == 800
+    assert _hip.query("ws_rmsnorm_backward_partial_floats", 10, 64) == 3 * 64
+
+
+def test_invalid_arguments_are_rejected_before_any_launch():
+    """Argument validation runs on the host and reports through ws_last_error."""
+    with pytest.raises(RuntimeError, match="positive"):
+        _hip.call("ws_mm", 16, 8, 1, 16, 8, 1, 16, 0, 8, 8, 0, 0, None)
+    with pytest.raises(RuntimeError, match="algorithm"):
+        _hip.call("ws_mm", 16, 8, 1, 16, 8, 1, 16, 8, 8, 8, 7, 0, None)
+    with pytest.raises(RuntimeError, match="gate column range"):
+        _hip.call("ws_rmsnorm_gate_mm", 16, 8, 16, 1e-6, 16, 16, 1, 8, 16, 8, 8, 8, 6, 9, None)

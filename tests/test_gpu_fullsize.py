@@ -1,0 +1,130 @@
+"""The five benchmark configurations at their full sizes on the GPU.
+
+The HIP path runs on the whole workload; the CPU oracle checks it on a spread sample of
+rows (every output row depends only on its own input row and the weights), or in full
+where that takes seconds (configs 1 and 4). Size-independent properties are checked on
+the whole output: zero weights give sigmoid(0) = 0.5 exactly on the gate slice, the
+residual bit-for-bit, ln(vocab) per valid token and a zero dHidden; a zero upstream
+gradient leaves FP32 accumulators bit-for-bit; the valid-token count is exact.
+Bars: BF16 max|d|/max|ref| <= 1e-2 and rel-RMS <= 3e-3; FP32 ||d||/||ref|| <= 1e-3.
+"""
+import math
+
+import pytest
+import torch
+
+from metrics import assert_bf16_close, assert_f32_close
+from oracle import reference as oracle
+from ops import benchmark_configs as cfg
+
+pytestmark = pytest.mark.gpu
+
+SAMPLE = torch.arange(7, 16384, 32)  # 512 rows spread over the 16384 tokens
+
+
+def test_config1_swiglu_forward_full():
+    from ops.matmul_epilogue import launch_swiglu_mm
+
+    inp = cfg.swiglu_forward_inputs(seed=0)
+    packed, act = launch_swiglu_mm(inp["x"].cuda(), inp["w_upgate"].cuda().T, "tiled",
+                                   (128, 128, 32, 8, 3), False)
+    torch.cuda.synchronize()
+    want_packed, want_act = oracle.swiglu_mm(inp["x"], inp["w_upgate"].T, False)
+    assert_bf16_close(packed, want_packed, "config1 packed")
+    assert_bf16_close(act, want_act, "config1 act")
+
+
+def test_config2_rmsnorm_gate_projection_full():
+    from ops.fused_execution import rmsnorm_gate_mm
+
+    inp = cfg.rms_projection_inputs(seed=0)
+    x, nw, w = inp["x"].cuda(), inp["norm_weight"].cuda(), inp["w"].cuda()
+    out, rstd = rmsnorm_gate_mm(x, nw, inp["eps"], w, inp["gate"])
+    torch.cuda.synchronize()
+    want = oracle.rmsnorm_gate_projection(inp["x"][SAMPLE], inp["norm_weight"], inp["eps"],
+                                          inp["w"], inp["gate"])
+    assert_bf16_close(out[SAMPLE.cuda()], want, "config2 sample rows")
+    assert_f32_close(rstd.cpu(), oracle.rms_rstd(inp["x"], inp["eps"]), "config2 rstd")
+    lo, hi = inp["gate"]
+    zero, _ = rmsnorm_gate_mm(x, nw, inp["eps"], torch.zeros_like(w), inp["gate"], out=out)
+    torch.cuda.synchronize()
+    assert torch.all(zero[:, lo:hi] == 0.5).item()
+    assert torch.count_nonzero(zero[:, :lo]).item() == 0
+    assert torch.count_nonzero(zero[:, hi:]).item() == 0
+
+
+def test_config3_down_residual_full():
+    from ops.fused_execution import residual_mm
+
+    inp = cfg.down_residual_inputs(seed=0)
+    h, w, r = inp["h"].cuda(), inp["w_down"].cuda(), inp["residual"].cuda()
+    out = residual_mm(h, w, r)
+    torch.cuda.synchronize()
+    want = oracle.residual_projection(inp["h"][SAMPLE], inp["w_down"], inp["residual"][SAMPLE])
+    assert_bf16_close(out[SAMPLE.cuda()], want, "config3 sample rows")
+    same = residual_mm(h, torch.zeros_like(w), r)
+    torch.cuda.synchronize()
+    assert torch.equal(same, r)
+
+
+def test_config4_mlp_backward_full():
+    from ops.fused_execution import mlp_backward
+    from ops.matmul_epilogue import launch_swiglu_mm
+
+    inp = cfg.mlp_backward_inputs(seed=0)
+    x, wug, wd, dy = (inp[k].cuda() for k in ("x", "w_upgate", "w_down", "dy"))
+    g_up, g_down = inp["g_upgate"].cuda(), inp["g_down"].cuda()
+    packed, act = launch_swiglu_mm(x, wug.T, "tiled", (128, 128, 32, 8, 3), True)
+    dx = mlp_backward(x, wug, wd, packed, act, dy, g_up, g_down)
+    torch.cuda.synchronize()
+    # The oracle consumes the same saved forward tensors (they are parity-checked in the
+    # forward tests), so the backward is compared on identical inputs.
+    want_dx, want_dpacked, want_up, want_down = oracle.mlp_backward(
+        inp["x"], inp["w_upgate"], inp["w_down"], packed.cpu(), act.cpu(), inp["dy"],
+        inp["g_upgate"], inp["g_down"])
+    assert_bf16_close(dx, want_dx, "config4 dX")
+    assert_f32_close(g_up.cpu(), want_up, "config4 G_upgate")
+    assert_f32_close(g_down.cpu(), want_down, "config4 G_down")
+    # The accumulation itself, net of the preloaded buffers.
+    assert_f32_close((g_up.cpu() - inp["g_upgate"]), want_up - inp["g_upgate"], "config4 dW_upgate")
+    assert_f32_close((g_down.cpu() - inp["g_down"]), want_down - inp["g_down"], "config4 dW_down")
+    before_up, before_down = g_up.clone(), g_down.clone()
+    mlp_backward(x, wug, wd, packed, act, torch.zeros_like(dy), g_up, g_down)
+    torch.cuda.synchronize()
+    assert torch.equal(g_up, before_up) and torch.equal(g_down, before_down)
+
+
+def test_config5_lm_head_cross_entropy_full():
+    from ops.fused_execution import linear_cross_entropy_backward, linear_cross_entropy_forward
+
+    inp = cfg.lm_head_inputs(seed=0)
+    hidden, weight, targets = (inp[k].cuda() for k in ("hidden", "weight", "targets"))
+    count = int(inp["targets"].ne(-100).sum())
+    assert count == 16384 - 819
+    state = linear_cross_entropy_forward(hidden, weight, targets)
+    sample_targets = inp["targets"][SAMPLE]
+    count_s = int(sample_targets.ne(-100).sum())
+    # Upstream gradient count/count_s makes the full-batch dHidden rows equal those of
+    # the sample's own mean, which is what the oracle computes on the sample.
+    grad = torch.full((), count / count_s, device="cuda")
+    dh = linear_cross_entropy_backward(hidden, weight, targets, state, grad)
+    torch.cuda.synchronize()
+    assert int(state.count.item()) == count
+    loss_s, mean_s, _, dh_s = oracle.linear_cross_entropy(inp["hidden"][SAMPLE], inp["weight"],
+                                                          sample_targets)
+    got = state.loss.cpu()
+    assert torch.allclose(got[SAMPLE], loss_s, rtol=1e-4, atol=1e-4)
+    assert torch.all(got[inp["targets"] == -100] == 0)
+    assert math.isclose(state.mean.item(), got.double().sum().item() / count, rel_tol=1e-5)
+    assert_bf16_close(dh[SAMPLE.cuda()], dh_s, "config5 dHidden sample rows")
+    # Zero head weight: every valid token costs ln(vocab); the gradient is zero.
+    zero_w = torch.zeros_like(weight)
+    state = linear_cross_entropy_forward(hidden, zero_w, targets, state)
+    dh0 = linear_cross_entropy_backward(hidden, zero_w, targets, state,
+                                        torch.ones((), device="cuda"), out=dh)
+    torch.cuda.synchronize()
+    valid = targets != -100
+    assert torch.allclose(state.loss[valid], torch.full((count,), math.log(32768), device="cuda"),
+                          rtol=1e-6)
+    assert abs(state.mean.item() - math.log(32768)) < 1e-5
+    assert torch.count_nonzero(dh0).item() == 0
