@@ -86,17 +86,18 @@ int ws_rms_rstd(const void* x, int64_t ldx, float* rstd, int64_t rows, int64_t d
                 void* stream);
 
 /*
- * RMSNorm-prologue projection with gate sigmoid: out[m,n] = bf16(y @ B) where
- * y = r(r(x * rstd) * r(norm_weight)) is formed in the GEMM's operand path and never
- * stored, then out[:, gate_begin:gate_end] = r(sigmoid(out)). Also writes rstd [m].
- * Restates RMSNorm.forward (warpstate/model.py:22-28) -> in_proj (warpstate/model.py:93,
- * 109) -> torch.sigmoid on the gate slice (warpstate/model.py:174). x needs a unit
- * column stride.
+ * RMSNorm-prologue projection with gate sigmoid: out[m,n] = bf16(y @ B) with
+ * y = r(r(x * rstd) * r(norm_weight)), then out[:, gate_begin:gate_end] = r(sigmoid(out)).
+ * The prologue is one pass over x that writes y into `normed` [m, k] (row-contiguous,
+ * caller-allocated; it is also the saved input of the projection's weight gradient) and
+ * rstd [m]; the GEMM then reads y. Restates RMSNorm.forward (warpstate/model.py:22-28) ->
+ * in_proj (warpstate/model.py:93, 109) -> torch.sigmoid on the gate slice
+ * (warpstate/model.py:174). x needs a unit column stride.
  */
 int ws_rmsnorm_gate_mm(const void* x, int64_t x_s0, const float* norm_weight, float eps,
-                       float* rstd, const void* b, int64_t b_s0, int64_t b_s1, void* out,
-                       int64_t m, int64_t n, int64_t k, int64_t gate_begin, int64_t gate_end,
-                       void* stream);
+                       float* rstd, void* normed, const void* b, int64_t b_s0, int64_t b_s1,
+                       void* out, int64_t m, int64_t n, int64_t k, int64_t gate_begin,
+                       int64_t gate_end, void* stream);
 
 /* Down projection with residual add: out[m,n] = r(residual[m,n] + r(A @ B)), residual
  * row stride ld_residual (warpstate/model.py:178 under BF16 residuals,
@@ -147,18 +148,22 @@ int ws_linear_ce_forward(const void* hidden, int64_t ld_hidden, const void* weig
                          int64_t d, float* part_max, float* part_sum, float* target_logit,
                          float* lse, float* loss, float* mean, float* count, void* stream);
 
+/* Bytes of the workspace ws_linear_ce_backward needs for `chunk_rows`-row chunks. */
+int64_t ws_linear_ce_workspace_bytes(int64_t rows, int64_t vocab, int64_t d, int64_t chunk_rows);
+
 /*
  * Fused LM-head cross-entropy backward: dhidden [rows, d] = r(r(g (softmax - onehot)) @ W)
- * with g = grad_mean / max(1, count), zero rows for ignored targets. Logit gradients are
- * formed chunk_rows rows at a time into grad_logits_ws [chunk_rows, vocab] BF16 and
- * consumed by the dhidden GEMM of that chunk; scale_ws holds one float.
- * Restates autograd of warpstate/model.py:321-334.
+ * with g = grad_mean / max(1, count), zero rows for ignored targets. Rows are processed
+ * chunk_rows at a time: the BF16 logit gradients of one chunk ([chunk_rows, vocab], never
+ * the whole batch) go to the 256-byte aligned `workspace` and feed that chunk's dHidden
+ * GEMM, split over the vocab with FP32 partials when the chunk alone would not fill the
+ * GPU. Restates autograd of warpstate/model.py:321-334.
  */
 int ws_linear_ce_backward(const void* hidden, int64_t ld_hidden, const void* weight,
                           int64_t ld_weight, const int64_t* targets, const float* lse,
                           const float* count, const float* grad_mean, int64_t rows,
-                          int64_t vocab, int64_t d, void* grad_logits_ws, int64_t chunk_rows,
-                          float* scale_ws, void* dhidden, int64_t ld_dhidden, void* stream);
+                          int64_t vocab, int64_t d, void* workspace, int64_t chunk_rows,
+                          void* dhidden, int64_t ld_dhidden, void* stream);
 
 #ifdef __cplusplus
 }

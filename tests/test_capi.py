@@ -48,6 +48,9 @@ def test_queries_without_device_work():
     assert _hip.query("ws_mm_accumulate_workspace_floats", 10, 20, 1) == 0
     assert _hip.query("ws_mm_accumulate_workspace_floats", 10, 20, 4) == 800
     assert _hip.query("ws_rmsnorm_backward_partial_floats", 10, 64) == 3 * 64
+    # One 4096-row chunk of BF16 logit gradients plus two FP32 dHidden partial slices.
+    assert _hip.query("ws_linear_ce_workspace_bytes", 16384, 32768, 2048, 4096) == \
+        256 + 4096 * 32768 * 2 + 2 * 4096 * 2048 * 4
 
 
 def test_invalid_arguments_are_rejected_before_any_launch():
@@ -57,4 +60,4 @@ def test_invalid_arguments_are_rejected_before_any_launch():
     with pytest.raises(RuntimeError, match="algorithm"):
         _hip.call("ws_mm", 16, 8, 1, 16, 8, 1, 16, 8, 8, 8, 7, 0, None)
     with pytest.raises(RuntimeError, match="gate column range"):
-        _hip.call("ws_rmsnorm_gate_mm", 16, 8, 16, 1e-6, 16, 16, 1, 8, 16, 8, 8, 8, 6, 9, None)
+        _hip.call("ws_rmsnorm_gate_mm", 16, 8, 16, 1e-6, 16, 16, 16, 1, 8, 16, 8, 8, 8, 6, 9, None)

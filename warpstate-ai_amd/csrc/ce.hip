@@ -48,9 +48,12 @@ extern "C" int ws_linear_ce_forward(const void* hidden, int64_t ld_hidden, const
   p.tgt_logit = target_logit;
   p.parts_per_row = (int)ws_linear_ce_parts(vocab);
   int am = operand_mode(p.a, rows, d, 256), bm = operand_mode(p.b, vocab, d, 256);
-  if (int rc = dispatch<kMaskKK | kMaskGG, WS_TILE_ARGS_LARGE, false, false, EpiCEStats>(
-          p, am, bm, LaunchCfg{0, 1}, s))
+  if (fast_ok(p, am, bm, false)) {
+    if (int rc = dispatch_fast<false, FEpiCEStats>(p, am, bm, LaunchCfg{0, 1}, s)) return rc;
+  } else if (int rc = dispatch<kMaskKK | kMaskGG, WS_TILE_ARGS_LARGE, false, false, EpiCEStats>(
+                 p, am, bm, LaunchCfg{0, 1}, s)) {
     return rc;
+  }
   hipLaunchKernelGGL(ce_combine_kernel, dim3(cdiv(rows, 4)), dim3(256), 0, s, part_max, part_sum,
                      p.parts_per_row, target_logit, reinterpret_cast<const long*>(targets), lse,
                      loss, (int)rows, (int)vocab);
@@ -60,23 +63,49 @@ extern "C" int ws_linear_ce_forward(const void* hidden, int64_t ld_hidden, const
   return hip_check(hipGetLastError(), "ce mean launch");
 }
 
+// Workspace of the backward: [scale, 256 B][chunk x vocab BF16 logit gradients]
+// [splits x chunk x d FP32 dHidden partials], each part 256-byte aligned.
+static inline long round256(long b) { return (b + 255) / 256 * 256; }
+
+// Split-K factor of a chunk's dHidden GEMM: enough workgroups to cover the CUs.
+static inline int ce_dh_splits(long chunk, long d, long vocab) {
+  const long tiles = (long)cdiv(chunk, 256) * cdiv(d, 256);
+  long splits = (256 + tiles - 1) / tiles;
+  const long k_tiles = cdiv(vocab, 64);
+  if (splits > 8) splits = 8;
+  if (splits > k_tiles / 4) splits = k_tiles / 4;
+  return splits < 1 ? 1 : (int)splits;
+}
+
+extern "C" int64_t ws_linear_ce_workspace_bytes(int64_t rows, int64_t vocab, int64_t d,
+                                                int64_t chunk_rows) {
+  const long chunk = chunk_rows < rows ? chunk_rows : rows;
+  const int splits = ce_dh_splits(chunk, d, vocab);
+  return 256 + round256(chunk * vocab * 2) + (splits > 1 ? round256((long)splits * chunk * d * 4) : 0);
+}
+
 extern "C" int ws_linear_ce_backward(const void* hidden, int64_t ld_hidden, const void* weight,
                                      int64_t ld_weight, const int64_t* targets, const float* lse,
                                      const float* count, const float* grad_mean, int64_t rows,
-                                     int64_t vocab, int64_t d, void* grad_logits_ws,
-                                     int64_t chunk_rows, float* scale_ws, void* dhidden,
-                                     int64_t ld_dhidden, void* stream) {
+                                     int64_t vocab, int64_t d, void* workspace,
+                                     int64_t chunk_rows, void* dhidden, int64_t ld_dhidden,
+                                     void* stream) {
   if (int rc = check_ce(hidden, ld_hidden, weight, ld_weight, targets, rows, vocab, d)) return rc;
-  if (!lse || !count || !grad_mean || !grad_logits_ws || !scale_ws || !dhidden)
-    return set_error(kInvalid, "null pointer");
-  if (chunk_rows < 1 || !fits_i32(chunk_rows * vocab / 1)) return set_error(kInvalid, "bad chunk_rows");
+  if (!lse || !count || !grad_mean || !workspace || !dhidden) return set_error(kInvalid, "null pointer");
+  if (chunk_rows < 1 || !fits_i32(chunk_rows * vocab)) return set_error(kInvalid, "bad chunk_rows");
   if (ld_dhidden < d) return set_error(kInvalid, "dhidden leading dimension < d");
+  if (reinterpret_cast<unsigned long>(workspace) % 256) return set_error(kInvalid, "workspace must be 256-byte aligned");
   hipStream_t s = static_cast<hipStream_t>(stream);
+  const long chunk = chunk_rows < rows ? chunk_rows : rows;
+  const int splits = ce_dh_splits(chunk, d, vocab);
+  auto* base = static_cast<unsigned char*>(workspace);
+  float* scale_ws = reinterpret_cast<float*>(base);
+  auto* gl = reinterpret_cast<unsigned short*>(base + 256);
+  float* partials = reinterpret_cast<float*>(base + 256 + round256(chunk * vocab * 2));
   hipLaunchKernelGGL(ce_scale_kernel, dim3(1), dim3(64), 0, s, grad_mean, count, scale_ws);
   if (int rc = hip_check(hipGetLastError(), "ce scale launch")) return rc;
-  auto* gl = static_cast<unsigned short*>(grad_logits_ws);
-  for (long start = 0; start < rows; start += chunk_rows) {
-    const long r = rows - start < chunk_rows ? rows - start : chunk_rows;
+  for (long start = 0; start < rows; start += chunk) {
+    const long r = rows - start < chunk ? rows - start : chunk;
     // Logit gradients of this row chunk, r(scale * (softmax - onehot)), BF16.
     GemmParams p{};
     p.a = OperandDesc{static_cast<const unsigned short*>(hidden) + start * ld_hidden, ld_hidden, 1};
@@ -84,27 +113,46 @@ extern "C" int ws_linear_ce_backward(const void* hidden, int64_t ld_hidden, cons
     p.M = (int)r; p.N = (int)vocab; p.K = (int)d;
     p.c = gl;
     p.ldc = vocab;
-    p.vec_out = (vocab % 4 == 0) && (reinterpret_cast<unsigned long>(gl) % 8 == 0);
+    p.vec_out = (vocab % 4 == 0);
     p.targets = reinterpret_cast<const long*>(targets) + start;
     p.lse = lse + start;
     p.grad_scale = scale_ws;
     int am = operand_mode(p.a, r, d, 256), bm = operand_mode(p.b, vocab, d, 256);
-    if (int rc = dispatch<kMaskKK | kMaskGG, WS_TILE_ARGS_LARGE, false, false, EpiCEGrad>(
-            p, am, bm, LaunchCfg{0, 1}, s))
+    if (fast_ok(p, am, bm, false)) {
+      if (int rc = dispatch_fast<false, FEpiCEGrad>(p, am, bm, LaunchCfg{0, 1}, s)) return rc;
+    } else if (int rc = dispatch<kMaskKK | kMaskGG, WS_TILE_ARGS_LARGE, false, false, EpiCEGrad>(
+                   p, am, bm, LaunchCfg{0, 1}, s)) {
       return rc;
-    // dHidden of the chunk: r(G [r, vocab] @ W [vocab, d]).
+    }
+    // dHidden of the chunk: r(G [r, vocab] @ W [vocab, d]), split over the vocab.
     GemmParams q{};
     q.a = OperandDesc{gl, vocab, 1};
     q.b = OperandDesc{static_cast<const unsigned short*>(weight), 1, ld_weight};
     q.M = (int)r; q.N = (int)d; q.K = (int)vocab;
-    q.c = static_cast<unsigned short*>(dhidden) + start * ld_dhidden;
-    q.ldc = ld_dhidden;
-    q.vec_out = (d % 4 == 0) && (ld_dhidden % 4 == 0) &&
-                (reinterpret_cast<unsigned long>(q.c) % 8 == 0);
-    int qa = operand_mode(q.a, r, vocab, 128), qb = operand_mode(q.b, d, vocab, 128);
-    if (int rc = dispatch<kMaskMM, WS_TILE_ARGS_SMALL, false, false, EpiStore<false, false>>(
-            q, qa, qb, LaunchCfg{0, 1}, s))
-      return rc;
+    unsigned short* out = static_cast<unsigned short*>(dhidden) + start * ld_dhidden;
+    int qa = operand_mode(q.a, r, vocab, 256), qb = operand_mode(q.b, d, vocab, 256);
+    const bool fast = fast_ok(q, qa, qb, false);
+    if (splits > 1 && fast) {
+      q.g = partials;
+      q.ldg = d;
+      q.split_stride = chunk * d;
+      q.vec_out = (d % 4 == 0);
+      if (int rc = dispatch_fast<false, FEpiAccF32<true>>(q, qa, qb, LaunchCfg{0, splits}, s)) return rc;
+      const long total = r * d;
+      hipLaunchKernelGGL(splitk_bf16_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
+                         partials, splits, (long)(chunk * d), out, (long)ld_dhidden, (int)r, (int)d);
+      if (int rc = hip_check(hipGetLastError(), "split-K reduce launch")) return rc;
+    } else {
+      q.c = out;
+      q.ldc = ld_dhidden;
+      q.vec_out = (d % 4 == 0) && (ld_dhidden % 4 == 0) && (reinterpret_cast<unsigned long>(out) % 8 == 0);
+      if (fast) {
+        if (int rc = dispatch_fast<false, FEpiStore<false, false>>(q, qa, qb, LaunchCfg{0, 1}, s)) return rc;
+      } else if (int rc = dispatch<kMaskMM, WS_TILE_ARGS_LARGE, false, false, EpiStore<false, false>>(
+                     q, qa, qb, LaunchCfg{0, 1}, s)) {
+        return rc;
+      }
+    }
   }
   return kOk;
 }

@@ -38,35 +38,36 @@ extern "C" int ws_rms_rstd(const void* x, int64_t ldx, float* rstd, int64_t rows
 }
 
 extern "C" int ws_rmsnorm_gate_mm(const void* x, int64_t x_s0, const float* norm_weight,
-                                  float eps, float* rstd, const void* b, int64_t b_s0,
-                                  int64_t b_s1, void* out, int64_t m, int64_t n, int64_t k,
-                                  int64_t gate_begin, int64_t gate_end, void* stream) {
+                                  float eps, float* rstd, void* normed, const void* b,
+                                  int64_t b_s0, int64_t b_s1, void* out, int64_t m, int64_t n,
+                                  int64_t k, int64_t gate_begin, int64_t gate_end, void* stream) {
   if (int rc = check_gemm_args(x, x_s0, 1, b, b_s0, b_s1, out, m, n, k)) return rc;
-  if (!norm_weight || !rstd) return set_error(kInvalid, "null RMSNorm pointer");
+  if (!norm_weight || !rstd || !normed) return set_error(kInvalid, "null RMSNorm pointer");
   if (gate_begin < 0 || gate_end < gate_begin || gate_end > n)
     return set_error(kInvalid, "gate column range [%ld, %ld) outside [0, %ld)", (long)gate_begin,
                      (long)gate_end, (long)n);
   if (x_s0 < k) return set_error(kInvalid, "RMSNorm prologue needs row-contiguous x");
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (int rc = launch_rstd(x, x_s0, rstd, m, k, eps, s)) return rc;
+  // Prologue: one pass over x writes the normalized BF16 operand y and rstd.
+  const int vec = (x_s0 % 8 == 0) && (k % 8 == 0) && al(x, 16) && al(normed, 16);
+  hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(cdiv(m, 4)), dim3(256), 0, s,
+                     static_cast<const unsigned short*>(x), (long)x_s0, norm_weight,
+                     static_cast<unsigned short*>(normed), rstd, (int)m, (int)k, eps, vec);
+  if (int rc = hip_check(hipGetLastError(), "rmsnorm rows launch")) return rc;
   GemmParams p{};
-  p.a = desc_a(x, x_s0, 1);
+  p.a = desc_a(normed, k, 1);
   p.b = desc_b(b, b_s0, b_s1);
   p.M = (int)m; p.N = (int)n; p.K = (int)k;
   p.c = static_cast<unsigned short*>(out);
   p.ldc = n;
   p.vec_out = (n % 4 == 0) && al(out, 8);
-  p.rstd = rstd;
-  p.norm_w = norm_weight;
   p.gate_lo = (int)gate_begin;
   p.gate_hi = (int)gate_end;
-  int am = operand_mode(p.a, m, k, 256);
-  if (am != kKContig)
-    return set_error(kInvalid, "RMSNorm prologue needs a 16-byte aligned x with k %% 8 == 0");
-  int bm = operand_mode(p.b, n, k, 256);
-  constexpr unsigned mask = kMaskKK | ab_bit(kKContig, kGeneric);
-  return dispatch<mask, WS_TILE_ARGS_LARGE, false, true, EpiStore<true, false>>(p, am, bm,
-                                                                                 LaunchCfg{0, 1}, s);
+  int am = operand_mode(p.a, m, k, 256), bm = operand_mode(p.b, n, k, 256);
+  if (fast_ok(p, am, bm, false))
+    return dispatch_fast<false, FEpiStore<true, false>>(p, am, bm, LaunchCfg{0, 1}, s);
+  return dispatch<kMaskMM, WS_TILE_ARGS_LARGE, false, false, EpiStore<true, false>>(p, am, bm,
+                                                                                   LaunchCfg{0, 1}, s);
 }
 
 extern "C" int ws_residual_mm(const void* a, int64_t a_s0, int64_t a_s1, const void* b,
@@ -85,9 +86,12 @@ extern "C" int ws_residual_mm(const void* a, int64_t a_s0, int64_t a_s1, const v
   p.ldaux = ld_residual;
   p.vec_out = (n % 4 == 0) && (ld_residual % 4 == 0) && al(out, 8) && al(residual, 8);
   int am = operand_mode(p.a, m, k, 256), bm = operand_mode(p.b, n, k, 256);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (fast_ok(p, am, bm, false))
+    return dispatch_fast<false, FEpiStore<false, true>>(p, am, bm, LaunchCfg{0, 1}, s);
   constexpr unsigned mask = kMaskKK | ab_bit(kKContig, kMNContig) | kMaskGG;
   return dispatch<mask, WS_TILE_ARGS_LARGE, false, false, EpiStore<false, true>>(
-      p, am, bm, LaunchCfg{0, 1}, static_cast<hipStream_t>(stream));
+      p, am, bm, LaunchCfg{0, 1}, s);
 }
 
 extern "C" int ws_swiglu_backward_mm(const void* grad, int64_t g_s0, int64_t g_s1, const void* b,
@@ -107,9 +111,12 @@ extern "C" int ws_swiglu_backward_mm(const void* grad, int64_t g_s0, int64_t g_s
   p.eager = eager_rounding ? 1 : 0;
   p.vec_out = (h % 4 == 0) && al(dpacked, 8) && al(packed, 8);
   int am = operand_mode(p.a, m, k, 256), bm = operand_mode(p.b, h, k, 256);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (fast_ok(p, am, bm, false))
+    return dispatch_fast<false, FEpiSwigluBwd>(p, am, bm, LaunchCfg{0, 1}, s);
   constexpr unsigned mask = kMaskKK | ab_bit(kKContig, kMNContig) | kMaskGG;
   return dispatch<mask, WS_TILE_ARGS_LARGE, false, false, EpiSwigluBwd>(
-      p, am, bm, LaunchCfg{0, 1}, static_cast<hipStream_t>(stream));
+      p, am, bm, LaunchCfg{0, 1}, s);
 }
 
 extern "C" int64_t ws_mm_accumulate_workspace_floats(int64_t m, int64_t n, int64_t splits) {
@@ -135,6 +142,8 @@ extern "C" int ws_mm_accumulate_f32(const void* a, int64_t a_s0, int64_t a_s1, c
     p.g = g;
     p.ldg = ldg;
     p.vec_out = (n % 4 == 0) && (ldg % 4 == 0) && al(g, 16);
+    if (fast_ok(p, am, bm, false))
+      return dispatch_fast<false, FEpiAccF32<false>>(p, am, bm, LaunchCfg{0, 1}, s);
     return dispatch<kMaskMM, WS_TILE_ARGS_LARGE, false, false, EpiAccF32<false>>(p, am, bm,
                                                                                   LaunchCfg{0, 1}, s);
   }
@@ -142,9 +151,13 @@ extern "C" int ws_mm_accumulate_f32(const void* a, int64_t a_s0, int64_t a_s1, c
   p.ldg = n;
   p.split_stride = m * n;
   p.vec_out = (n % 4 == 0) && al(workspace, 16);
-  if (int rc = dispatch<kMaskMM, WS_TILE_ARGS_LARGE, false, false, EpiAccF32<true>>(
-          p, am, bm, LaunchCfg{0, (int)splits}, s))
+  if (fast_ok(p, am, bm, false)) {
+    if (int rc = dispatch_fast<false, FEpiAccF32<true>>(p, am, bm, LaunchCfg{0, (int)splits}, s))
+      return rc;
+  } else if (int rc = dispatch<kMaskMM, WS_TILE_ARGS_LARGE, false, false, EpiAccF32<true>>(
+                 p, am, bm, LaunchCfg{0, (int)splits}, s)) {
     return rc;
+  }
   long total = m * n;
   hipLaunchKernelGGL(splitk_accum_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
                      workspace, (int)splits, (long)(m * n), g, (long)ldg, (int)m, (int)n,

@@ -11,8 +11,12 @@
 // Layout of one workgroup (BM x BN macro-tile, BK = 64):
 //  * LDS holds two stages of the A tile [BM rows][64 k] and the B tile [BN rows][64 k]
 //    (B is stored n-major, i.e. as B^T), k contiguous. Each 128-byte row is split into
-//    eight 16-byte chunks; chunk c of row r lives at chunk slot (c ^ (r & 7)), which
-//    makes both the 16-byte fragment reads and the tile writes bank-conflict free.
+//    eight 16-byte chunks; chunk c of row r lives at chunk slot c ^ swz(r) with
+//    swz(r) = (r >> 1) ^ ((r & 1) << 2) (mod 8). The LDS serves a 16-byte read for 16
+//    lanes per clock across its 64 banks; a fragment read has those 16 lanes on 16
+//    consecutive rows of one chunk, and swz makes (r & 1, slot) distinct over any 16
+//    consecutive rows (and the slot alone distinct over any 8), so fragment reads and
+//    tile writes are bank-conflict free.
 //  * Operands whose reduction dim is contiguous (row-major X, or W^T of an nn.Linear
 //    weight) are copied with 16-byte buffer loads straight into that layout. Operands
 //    whose reduction dim is strided (dY^T and X in weight gradients, W in input
@@ -92,6 +96,9 @@ __device__ __forceinline__ void tile_position(int t, int tiles_m, int tiles_n, i
   tn = within / actual;
 }
 
+// Chunk-slot swizzle of LDS tile row r (see the header comment).
+__device__ __forceinline__ int swz(int r) { return ((r >> 1) ^ ((r & 1) << 2)) & 7; }
+
 // --------------------------------------------------------------------------------------
 // Global -> LDS tile loaders. `R` tile rows, `NT` threads. `rows_valid` bounds the rows;
 // with `PAIRED`, tile rows [0, R/2) map to rows row0 + r and rows [R/2, R) map to
@@ -139,7 +146,7 @@ struct TileLoader<R, NT, kKContig, PAIRED> {
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
       int r = (tid >> 3) + i * (NT / 8);
-      *reinterpret_cast<u32x4_t*>(lds + r * kBK + ((c ^ (r & 7)) << 3)) = regs[i];
+      *reinterpret_cast<u32x4_t*>(lds + r * kBK + ((c ^ swz(r)) << 3)) = regs[i];
     }
   }
 };
@@ -163,7 +170,7 @@ __device__ __forceinline__ void store_units(unsigned short* lds, int rc, int kq,
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     int r = 8 * rc + e;
-    *reinterpret_cast<u32x2_t*>(lds + r * kBK + ((((kq >> 1) ^ e)) << 3) + ((kq & 1) << 2)) = w[e];
+    *reinterpret_cast<u32x2_t*>(lds + r * kBK + ((((kq >> 1) ^ swz(r))) << 3) + ((kq & 1) << 2)) = w[e];
   }
 }
 
@@ -698,7 +705,7 @@ gemm_kernel(const GemmParams p) {
     }
     b_row[j] = (r + (lane & 31)) * kBK;
   }
-  const int hi = lane >> 5, sw = lane & 7;
+  const int hi = lane >> 5, sw = swz(lane & 15);
 
   const int bn_cols = PAIRED ? BN / 2 : BN;  // output columns per tile
   const int k_tiles_total = cdiv(p.K, kBK);

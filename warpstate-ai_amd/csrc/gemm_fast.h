@@ -1,0 +1,549 @@
+// Fast-path BF16 GEMM for gfx950: direct-to-LDS operand loads, 16x16x32 MFMA.
+//
+// C[m, n] = sum_k A[m, k] B[k, n] with FP32 accumulation and the same epilogues as
+// gemm.h, for operands whose reduction dim or row dim is contiguous (every layout the
+// training step produces: X and W^T are K-contiguous; dY^T, X in weight gradients and W
+// in input gradients are M/N-contiguous).
+//
+// Workgroup: 256 x 256 output tile, BK = 64, 8 waves on a 4 x 2 grid (wave tile 64 x 128),
+// two LDS stages of 64 KiB (A 32 KiB + B 32 KiB).
+//  * Loads: `buffer_load_dword x4 ... lds` writes 16 bytes per lane straight into LDS at
+//    M0 + 16 * lane; the choice of global address per lane implements the LDS swizzle.
+//    Out-of-range rows, columns and k take an offset beyond the buffer's range and land
+//    as zeros.
+//  * K-contiguous operand tile: [rows][64 k], 128-byte rows of eight 16-byte chunks,
+//    chunk c of row r at slot c ^ swz(r) (gemm.h). Fragments are one ds_read_b128.
+//  * M/N-contiguous operand tile: [64 k][rows], 512-byte rows of 32 chunks (8 rows of
+//    the operand each), chunk c of k-row kk at slot c ^ 2 wtr(kk),
+//    wtr(kk) = (kk & 3) | ((kk >> 3 & 1) << 2). Fragments are two ds_read_b64_tr_b16:
+//    within each 16-lane group the transposing read hands element q of the 8 bytes
+//    addressed by lane L to lane 4 (L & 3) + q, slot L >> 2, so lane L addressing k-row
+//    k0 + (L >> 2), rows 4 (L & 3) .. + 3 leaves each lane four consecutive k of one row.
+//    The swizzle puts the four k-rows (and the next group's four) of one read on
+//    distinct 32-byte bank windows.
+//  * MFMA v_mfma_f32_16x16x32_bf16 with the B fragment as the instruction's A operand:
+//    lane l then holds output row m = m0 + 16 i + (l & 15), columns n0 + 16 j + 4 (l >> 4)
+//    + e, e = 0..3, which the epilogues store as 8-byte (BF16) or 16-byte (FP32) vectors.
+//  * Pipeline per k-tile: wait for this wave's loads of the tile, s_barrier (no memory
+//    fence: the explicit vmcnt wait is the only ordering needed), issue the next tile's
+//    loads into the other stage, then the two k32 steps with the second step's fragment
+//    reads interleaved between the first step's MFMAs.
+//  * Tiles follow the grouped raster of ops/matmul_kernels.py:72-78 after an XCD remap.
+#pragma once
+
+#include "gemm.h"
+
+namespace ws {
+
+constexpr int kFBM = 256, kFBN = 256, kFBK = 64, kFWM = 4, kFWN = 2;
+constexpr int kFNT = kFWM * kFWN * kWave;               // 512 threads
+constexpr int kFTileBytes = 256 * kFBK * 2;             // one operand tile, 32 KiB
+constexpr int kFStageBytes = 2 * kFTileBytes;
+constexpr int kFLdsBytes = 2 * kFStageBytes;            // 128 KiB
+constexpr int kFIns = kFTileBytes / (kFNT * 16);         // 4 loads per thread per operand
+
+typedef float f32x4_v __attribute__((ext_vector_type(4)));
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ int wtr(int kk) { return (kk & 3) | (((kk >> 3) & 1) << 2); }
+
+// waitcnt immediate for "vmcnt <= n" leaving the other counters unconstrained (gfx9).
+constexpr int wait_vmcnt(int n) { return (n & 0xF) | (7 << 4) | (0xF << 8) | ((n >> 4) << 14); }
+
+#define WS_LDS(p) ((__attribute__((address_space(3))) void*)(p))
+
+// Direct-to-LDS loader of one 256-row operand tile. `off[i]` is the byte offset of this
+// lane's 16-byte chunk for load i relative to the tile's global base at k0, or kOOB.
+template <int MODE, bool PAIRED>
+struct DmaTile {
+  unsigned off[kFIns];
+
+  // k offset within the tile of load i's chunk: 8 c (K-contiguous) or the k-row kk.
+  __device__ __forceinline__ static int k_of(int i, int wave, int lane) {
+    const int byte = (i * (kFNT / kWave) + wave) * 1024 + lane * 16;
+    if constexpr (MODE == kKContig) return 8 * (((byte >> 4) & 7) ^ swz(byte >> 7));
+    else return byte >> 9;
+  }
+  __device__ __forceinline__ void init(const OperandDesc& d, int row0, int rows_valid, int half,
+                                       int wave, int lane) {
+#pragma unroll
+    for (int i = 0; i < kFIns; ++i) {
+      const int byte = (i * (kFNT / kWave) + wave) * 1024 + lane * 16;
+      if constexpr (MODE == kKContig) {
+        const int r = byte >> 7, c = ((byte >> 4) & 7) ^ swz(r);
+        const int logical = row0 + (PAIRED && r >= 128 ? r - 128 : r);
+        const int phys = PAIRED && r >= 128 ? half + logical : logical;
+        off[i] = logical < rows_valid ? (unsigned)((long)(phys - row0) * d.s_row * 2 + 16 * c) : kOOB;
+      } else {
+        const int kk = byte >> 9, c = ((byte >> 4) & 31) ^ (2 * wtr(kk));
+        const int r = 8 * c;  // first operand row of the chunk
+        const int logical = row0 + (PAIRED && r >= 128 ? r - 128 : r);
+        const int phys = PAIRED && r >= 128 ? half + logical : logical;
+        off[i] = logical < rows_valid ? (unsigned)((phys - row0) * 2 + (long)kk * d.s_k * 2) : kOOB;
+      }
+    }
+  }
+  // Loads of the tile at k0 into `lds_tile`; chunks at k >= K load zeros. The per-lane k
+  // test only runs on a ragged last tile.
+  __device__ __forceinline__ void issue(const OperandDesc& d, int row0, int k0, int K,
+                                        unsigned char* lds_tile, int wave, int lane) const {
+    const unsigned short* base =
+        MODE == kKContig ? d.ptr + (long)row0 * d.s_row + k0 : d.ptr + row0 + (long)k0 * d.s_k;
+    __amdgpu_buffer_rsrc_t rs = make_rsrc(base, 0x7fffffff);
+    const bool ragged = k0 + kFBK > K;
+#pragma unroll
+    for (int i = 0; i < kFIns; ++i) {
+      unsigned o = off[i];
+      if (ragged && k0 + k_of(i, wave, lane) >= K) o = kOOB;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, WS_LDS(lds_tile + (i * (kFNT / kWave) + wave) * 1024),
+                                               16, o, 0, 0, 0);
+    }
+  }
+};
+
+// Fragment reads for 16-row block at tile row `rb` (multiple of 16), k32 step s.
+template <int MODE>
+__device__ __forceinline__ bf16x8_t read_frag(const unsigned char* tile, int rb, int s, int lane) {
+  if constexpr (MODE == kKContig) {
+    const int r = rb + (lane & 15);
+    const int c = (4 * s + (lane >> 4)) ^ swz(r);
+    return *reinterpret_cast<const bf16x8_t*>(tile + r * 128 + c * 16);
+  } else {
+    const int L = lane & 15, g = lane >> 4;
+    const int m = rb + 4 * (L & 3);
+    const int kk0 = 32 * s + 8 * g + (L >> 2);
+    const int kk1 = kk0 + 4;
+    const int c = m >> 3, hb = (m & 4) * 2;  // byte within chunk: 0 or 8
+    const unsigned char* p0 = tile + kk0 * 512 + ((c ^ (2 * wtr(kk0))) << 4) + hb;
+    const unsigned char* p1 = tile + kk1 * 512 + ((c ^ (2 * wtr(kk1))) << 4) + hb;
+    i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) i16x4_t*)(p0));
+    i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) i16x4_t*)(p1));
+    typedef short i16x8_t __attribute__((ext_vector_type(8)));
+    i16x8_t v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    return __builtin_bit_cast(bf16x8_t, v);
+  }
+}
+
+template <int FA, int FB>
+struct Acc16 {
+  f32x4_v v[FA][FB];
+};
+
+// --------------------------------------------------------------------------------------
+// Epilogues on the 16x16 accumulator layout. Lane l holds, for block (i, j), row
+//   m = m_base + 16 i + (l & 15) and columns n = n_base + 16 j + 4 (l >> 4) + e.
+
+// Plain BF16 store with optional column-range sigmoid and BF16 residual add
+// (same numerics as EpiStore).
+template <bool SIGMOID, bool RESIDUAL>
+struct FEpiStore {
+  template <int FA, int FB>
+  __device__ __forceinline__ static void run(const GemmParams& p, Acc16<FA, FB>& acc, int m_base,
+                                             int n_base, int lane, int tm, int tn, int wn) {
+    const int m0 = tm * kFBM, n0 = tn * kFBN;
+    unsigned short* cbase = p.c + (long)m0 * p.ldc + n0;
+    __amdgpu_buffer_rsrc_t rc = make_rsrc(cbase, 0x7fffffff);
+    const unsigned short* rbase = RESIDUAL ? p.aux + (long)m0 * p.ldaux + n0 : cbase;
+    __amdgpu_buffer_rsrc_t rr = make_rsrc(rbase, 0x7fffffff);
+#pragma unroll
+    for (int i = 0; i < FA; ++i) {
+      const int m = m_base + 16 * i + (lane & 15);
+      const bool mok = m < p.M;
+#pragma unroll
+      for (int j = 0; j < FB; ++j) {
+        const int n = n_base + 16 * j + 4 * (lane >> 4);
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float x = acc.v[i][j][e];
+          if (SIGMOID) {
+            x = rbf16(x);
+            if (n + e >= p.gate_lo && n + e < p.gate_hi) x = sigmoid(x);
+          }
+          v[e] = x;
+        }
+        if (p.vec_out) {
+          const bool ok = mok && (n + 3 < p.N);
+          if (RESIDUAL) {
+            u32x2_t rv = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(
+                rr, store_off(ok, (long)(m - m0) * p.ldaux + (n - n0), 2), 0, 0));
+            v[0] = rbf16(v[0]) + lo_bf16(rv[0]);
+            v[1] = rbf16(v[1]) + hi_bf16(rv[0]);
+            v[2] = rbf16(v[2]) + lo_bf16(rv[1]);
+            v[3] = rbf16(v[3]) + hi_bf16(rv[1]);
+          }
+          u32x2_t out = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+          __builtin_amdgcn_raw_buffer_store_b64(out, rc,
+                                                store_off(ok, (long)(m - m0) * p.ldc + (n - n0), 2), 0, 0);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const bool ok = mok && (n + e < p.N);
+            float x = v[e];
+            if (RESIDUAL && ok) x = rbf16(x) + bf16_bits_to_f32(rbase[(long)(m - m0) * p.ldaux + (n + e - n0)]);
+            if (ok) cbase[(long)(m - m0) * p.ldc + (n + e - n0)] = to_bf16_bits(x);
+          }
+        }
+      }
+    }
+  }
+};
+
+// Paired SwiGLU forward (EpiSwiglu numerics): blocks j < FB/2 are up columns, j + FB/2
+// the gate columns of the same output columns.
+struct FEpiSwiglu {
+  template <int FA, int FB>
+  __device__ __forceinline__ static void run(const GemmParams& p, Acc16<FA, FB>& acc, int m_base,
+                                             int n_base, int lane, int tm, int tn, int wn) {
+    constexpr int FH = FB / 2;
+    const int m0 = tm * kFBM, n0 = tn * (kFBN / 2);
+    unsigned short* pbase = p.c + (long)m0 * p.ldc + n0;
+    unsigned short* abase = p.c2 + (long)m0 * p.ldc2 + n0;
+    __amdgpu_buffer_rsrc_t rp = make_rsrc(pbase, 0x7fffffff);
+    __amdgpu_buffer_rsrc_t ra = make_rsrc(abase, 0x7fffffff);
+    const long hoff = p.H;
+#pragma unroll
+    for (int i = 0; i < FA; ++i) {
+      const int m = m_base + 16 * i + (lane & 15);
+      const bool mok = m < p.M;
+#pragma unroll
+      for (int j = 0; j < FH; ++j) {
+        const int n = n_base + 16 * j + 4 * (lane >> 4);
+        float up[4], gate[4], act[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          up[e] = rbf16(acc.v[i][j][e]);
+          gate[e] = rbf16(acc.v[i][j + FH][e]);
+          float s = silu(gate[e]);
+          if (p.eager) s = rbf16(s);
+          act[e] = s * up[e];
+        }
+        if (p.vec_out) {
+          const bool ok = mok && (n + 3 < p.H);
+          const long rowp = (long)(m - m0) * p.ldc + (n - n0);
+          u32x2_t vu = {pack_bf16x2(up[0], up[1]), pack_bf16x2(up[2], up[3])};
+          u32x2_t vg = {pack_bf16x2(gate[0], gate[1]), pack_bf16x2(gate[2], gate[3])};
+          u32x2_t va = {pack_bf16x2(act[0], act[1]), pack_bf16x2(act[2], act[3])};
+          __builtin_amdgcn_raw_buffer_store_b64(vu, rp, store_off(ok, rowp, 2), 0, 0);
+          __builtin_amdgcn_raw_buffer_store_b64(vg, rp, store_off(ok, rowp + hoff, 2), 0, 0);
+          __builtin_amdgcn_raw_buffer_store_b64(
+              va, ra, store_off(ok, (long)(m - m0) * p.ldc2 + (n - n0), 2), 0, 0);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            if (mok && n + e < p.H) {
+              const long rowp = (long)(m - m0) * p.ldc + (n + e - n0);
+              pbase[rowp] = to_bf16_bits(up[e]);
+              pbase[rowp + hoff] = to_bf16_bits(gate[e]);
+              abase[(long)(m - m0) * p.ldc2 + (n + e - n0)] = to_bf16_bits(act[e]);
+            }
+          }
+        }
+      }
+    }
+  }
+};
+
+// SwiGLU backward on the dAct GEMM (EpiSwigluBwd numerics).
+struct FEpiSwigluBwd {
+  template <int FA, int FB>
+  __device__ __forceinline__ static void run(const GemmParams& p, Acc16<FA, FB>& acc, int m_base,
+                                             int n_base, int lane, int tm, int tn, int wn) {
+    const int m0 = tm * kFBM, n0 = tn * kFBN;
+    unsigned short* dbase = p.c + (long)m0 * p.ldc + n0;
+    const unsigned short* pbase = p.aux + (long)m0 * p.ldaux + n0;
+    __amdgpu_buffer_rsrc_t rd = make_rsrc(dbase, 0x7fffffff);
+    __amdgpu_buffer_rsrc_t rp = make_rsrc(pbase, 0x7fffffff);
+    const long hoff = p.H;
+#pragma unroll
+    for (int i = 0; i < FA; ++i) {
+      const int m = m_base + 16 * i + (lane & 15);
+      const bool mok = m < p.M;
+#pragma unroll
+      for (int j = 0; j < FB; ++j) {
+        const int n = n_base + 16 * j + 4 * (lane >> 4);
+        const bool ok4 = mok && (n + 3 < p.N);
+        float up[4], gate[4];
+        if (p.vec_out) {
+          const long rowp = (long)(m - m0) * p.ldaux + (n - n0);
+          u32x2_t vu = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(
+              rp, store_off(ok4, rowp, 2), 0, 0));
+          u32x2_t vg = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(
+              rp, store_off(ok4, rowp + hoff, 2), 0, 0));
+          up[0] = lo_bf16(vu[0]); up[1] = hi_bf16(vu[0]); up[2] = lo_bf16(vu[1]); up[3] = hi_bf16(vu[1]);
+          gate[0] = lo_bf16(vg[0]); gate[1] = hi_bf16(vg[0]); gate[2] = lo_bf16(vg[1]); gate[3] = hi_bf16(vg[1]);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const bool ok = mok && (n + e < p.N);
+            const long rowp = (long)(m - m0) * p.ldaux + (n + e - n0);
+            up[e] = ok ? bf16_bits_to_f32(pbase[rowp]) : 0.0f;
+            gate[e] = ok ? bf16_bits_to_f32(pbase[rowp + hoff]) : 0.0f;
+          }
+        }
+        float du[4], dg[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float dy = rbf16(acc.v[i][j][e]);
+          const float sg = sigmoid(gate[e]);
+          float s = silu(gate[e]);
+          if (p.eager) s = rbf16(s);
+          float dsilu = dy * up[e];
+          if (p.eager) dsilu = rbf16(dsilu);
+          du[e] = dy * s;
+          dg[e] = (dsilu * sg) * (1.0f + gate[e] * (1.0f - sg));
+        }
+        if (p.vec_out) {
+          const long rowd = (long)(m - m0) * p.ldc + (n - n0);
+          u32x2_t vu = {pack_bf16x2(du[0], du[1]), pack_bf16x2(du[2], du[3])};
+          u32x2_t vg = {pack_bf16x2(dg[0], dg[1]), pack_bf16x2(dg[2], dg[3])};
+          __builtin_amdgcn_raw_buffer_store_b64(vu, rd, store_off(ok4, rowd, 2), 0, 0);
+          __builtin_amdgcn_raw_buffer_store_b64(vg, rd, store_off(ok4, rowd + hoff, 2), 0, 0);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            if (mok && n + e < p.N) {
+              const long rowd = (long)(m - m0) * p.ldc + (n + e - n0);
+              dbase[rowd] = to_bf16_bits(du[e]);
+              dbase[rowd + hoff] = to_bf16_bits(dg[e]);
+            }
+          }
+        }
+      }
+    }
+  }
+};
+
+// FP32 accumulation (EpiAccF32 numerics); raw FP32 split-K partials when SPLIT.
+template <bool SPLIT>
+struct FEpiAccF32 {
+  template <int FA, int FB>
+  __device__ __forceinline__ static void run(const GemmParams& p, Acc16<FA, FB>& acc, int m_base,
+                                             int n_base, int lane, int tm, int tn, int wn) {
+    const int m0 = tm * kFBM, n0 = tn * kFBN;
+    float* gbase = p.g + (SPLIT ? (long)blockIdx.y * p.split_stride : 0) + (long)m0 * p.ldg + n0;
+    __amdgpu_buffer_rsrc_t rg = make_rsrc(gbase, 0x7fffffff);
+#pragma unroll
+    for (int i = 0; i < FA; ++i) {
+      const int m = m_base + 16 * i + (lane & 15);
+      const bool mok = m < p.M;
+#pragma unroll
+      for (int j = 0; j < FB; ++j) {
+        const int n = n_base + 16 * j + 4 * (lane >> 4);
+        if (p.vec_out) {
+          const bool ok = mok && (n + 3 < p.N);
+          const unsigned off = store_off(ok, (long)(m - m0) * p.ldg + (n - n0), 4);
+          f32x4_t add;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float x = acc.v[i][j][e];
+            add[e] = (!SPLIT && p.round_acc) ? rbf16(x) : x;
+          }
+          if (!SPLIT) {
+            f32x4_t old = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rg, off, 0, 0));
+            add = old + add;
+          }
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, add), rg, off, 0, 0);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            if (mok && n + e < p.N) {
+              const float x = acc.v[i][j][e];
+              float* dst = gbase + (long)(m - m0) * p.ldg + (n + e - n0);
+              if (SPLIT) *dst = x;
+              else *dst += p.round_acc ? rbf16(x) : x;
+            }
+          }
+        }
+      }
+    }
+  }
+};
+
+// LM-head pass 1 (EpiCEStats numerics): per row, over this wave's 128 columns of BF16
+// logits, the max and the sum of exp(l - max), one partial per (row, wave column block),
+// and the target's logit. The four lanes l, l^16, l^32, l^48 share a row.
+struct FEpiCEStats {
+  template <int FA, int FB>
+  __device__ __forceinline__ static void run(const GemmParams& p, Acc16<FA, FB>& acc, int m_base,
+                                             int n_base, int lane, int tm, int tn, int wn) {
+    const int part = tn * kFWN + wn;
+#pragma unroll
+    for (int i = 0; i < FA; ++i) {
+      const int m = m_base + 16 * i + (lane & 15);
+      const bool mok = m < p.M;
+      const long tgt = mok ? p.targets[m] : -1;
+      float mx = -INFINITY;
+#pragma unroll
+      for (int j = 0; j < FB; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int n = n_base + 16 * j + 4 * (lane >> 4) + e;
+          const float x = rbf16(acc.v[i][j][e]);
+          acc.v[i][j][e] = x;
+          if (n < p.N) mx = fmaxf(mx, x);
+          if ((long)n == tgt && n < p.N) p.tgt_logit[m] = x;
+        }
+      mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+      float sum = 0.0f;
+#pragma unroll
+      for (int j = 0; j < FB; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int n = n_base + 16 * j + 4 * (lane >> 4) + e;
+          if (n < p.N) sum += exp_e(acc.v[i][j][e] - mx);
+        }
+      sum += __shfl_xor(sum, 16, kWave);
+      sum += __shfl_xor(sum, 32, kWave);
+      if (mok && lane < 16) {
+        p.part_max[(long)m * p.parts_per_row + part] = mx;
+        p.part_sum[(long)m * p.parts_per_row + part] = sum;
+      }
+    }
+  }
+};
+
+// LM-head pass 2 (EpiCEGrad numerics): r(scale * (softmax - onehot)), 0 for ignored rows.
+struct FEpiCEGrad {
+  template <int FA, int FB>
+  __device__ __forceinline__ static void run(const GemmParams& p, Acc16<FA, FB>& acc, int m_base,
+                                             int n_base, int lane, int tm, int tn, int wn) {
+    const int m0 = tm * kFBM, n0 = tn * kFBN;
+    unsigned short* cbase = p.c + (long)m0 * p.ldc + n0;
+    __amdgpu_buffer_rsrc_t rc = make_rsrc(cbase, 0x7fffffff);
+#pragma unroll
+    for (int i = 0; i < FA; ++i) {
+      const int m = m_base + 16 * i + (lane & 15);
+      const bool mok = m < p.M;
+      const long tgt = mok ? p.targets[m] : -100;
+      const float lse = mok ? p.lse[m] : 0.0f;
+      const float scale = (tgt == -100) ? 0.0f : *p.grad_scale;
+#pragma unroll
+      for (int j = 0; j < FB; ++j) {
+        const int n = n_base + 16 * j + 4 * (lane >> 4);
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float l = rbf16(acc.v[i][j][e]);
+          v[e] = scale * exp_e(l - lse) - ((long)(n + e) == tgt ? scale : 0.0f);
+        }
+        if (p.vec_out) {
+          const bool ok = mok && (n + 3 < p.N);
+          u32x2_t out = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+          __builtin_amdgcn_raw_buffer_store_b64(out, rc,
+                                                store_off(ok, (long)(m - m0) * p.ldc + (n - n0), 2), 0, 0);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (mok && n + e < p.N) cbase[(long)(m - m0) * p.ldc + (n + e - n0)] = to_bf16_bits(v[e]);
+        }
+      }
+    }
+  }
+};
+
+// --------------------------------------------------------------------------------------
+// The kernel.
+
+template <int AMODE, int BMODE, bool PAIRED, class Epi>
+__global__ void __launch_bounds__(kFNT) gemm_fast_kernel(const GemmParams p) {
+  static_assert(AMODE != kGeneric && BMODE != kGeneric, "fast path needs vector operands");
+  constexpr int TM = kFBM / kFWM, TN = kFBN / kFWN;  // 64 x 128
+  constexpr int FA = TM / 16, FB = TN / 16;          // 4 x 8
+  constexpr int RA = AMODE == kKContig ? 1 : 2, RB = BMODE == kKContig ? 1 : 2;
+  constexpr int NR = FA * RA + FB * RB;              // DS read instructions per k32 step
+  constexpr int NM = FA * FB;                        // MFMAs per k32 step
+
+  extern __shared__ __attribute__((aligned(1024))) unsigned char fsmem[];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / kFWN, wn = wave % kFWN;
+  const int bn_cols = PAIRED ? kFBN / 2 : kFBN;
+  const int k_tiles_total = cdiv(p.K, kFBK);
+  const int kt_begin = blockIdx.y * p.k_tiles_per_split;
+  const int kt_end = min(k_tiles_total, kt_begin + p.k_tiles_per_split);
+
+  DmaTile<AMODE, false> la;
+  DmaTile<BMODE, PAIRED> lb;
+
+  // Tile rows of this wave's fragments (B rows for paired tiles: up blocks then gate).
+  int b_rb[FB];
+#pragma unroll
+  for (int j = 0; j < FB; ++j) {
+    if (PAIRED) b_rb[j] = (j < FB / 2) ? wn * (TN / 2) + 16 * j : 128 + wn * (TN / 2) + 16 * (j - FB / 2);
+    else b_rb[j] = wn * TN + 16 * j;
+  }
+
+  for (int w = blockIdx.x; w < p.total_tiles; w += gridDim.x) {
+    const int t = xcd_remap(w, p.total_tiles, gridDim.x);
+    int tm, tn;
+    tile_position(t, p.tiles_m, p.tiles_n, tm, tn);
+    const int row0_a = tm * kFBM;
+    const int row0_b = tn * bn_cols;
+    la.init(p.a, row0_a, p.M, 0, wave, lane);
+    lb.init(p.b, row0_b, PAIRED ? p.H : p.N, PAIRED ? p.H : 0, wave, lane);
+
+    Acc16<FA, FB> acc;
+#pragma unroll
+    for (int i = 0; i < FA; ++i)
+#pragma unroll
+      for (int j = 0; j < FB; ++j) acc.v[i][j] = f32x4_v{0.f, 0.f, 0.f, 0.f};
+
+    if (kt_begin < kt_end) {
+      la.issue(p.a, row0_a, kt_begin * kFBK, p.K, fsmem, wave, lane);
+      lb.issue(p.b, row0_b, kt_begin * kFBK, p.K, fsmem + kFTileBytes, wave, lane);
+      for (int kt = kt_begin; kt < kt_end; ++kt) {
+        const int cur = (kt - kt_begin) & 1;
+        __builtin_amdgcn_s_waitcnt(wait_vmcnt(0));
+        __builtin_amdgcn_s_barrier();
+        if (kt + 1 < kt_end) {
+          unsigned char* nxt = fsmem + (cur ^ 1) * kFStageBytes;
+          la.issue(p.a, row0_a, (kt + 1) * kFBK, p.K, nxt, wave, lane);
+          lb.issue(p.b, row0_b, (kt + 1) * kFBK, p.K, nxt + kFTileBytes, wave, lane);
+        }
+        const unsigned char* sa = fsmem + cur * kFStageBytes;
+        const unsigned char* sb = sa + kFTileBytes;
+        bf16x8_t af[2][FA], bfr[2][FB];
+#pragma unroll
+        for (int i = 0; i < FA; ++i) af[0][i] = read_frag<AMODE>(sa, wm * TM + 16 * i, 0, lane);
+#pragma unroll
+        for (int j = 0; j < FB; ++j) bfr[0][j] = read_frag<BMODE>(sb, b_rb[j], 0, lane);
+#pragma unroll
+        for (int s = 0; s < kFBK / 32; ++s) {
+          if (s + 1 < kFBK / 32) {
+#pragma unroll
+            for (int i = 0; i < FA; ++i) af[(s + 1) & 1][i] = read_frag<AMODE>(sa, wm * TM + 16 * i, s + 1, lane);
+#pragma unroll
+            for (int j = 0; j < FB; ++j) bfr[(s + 1) & 1][j] = read_frag<BMODE>(sb, b_rb[j], s + 1, lane);
+          }
+#pragma unroll
+          for (int i = 0; i < FA; ++i)
+#pragma unroll
+            for (int j = 0; j < FB; ++j)
+              acc.v[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bfr[s & 1][j], af[s & 1][i],
+                                                                     acc.v[i][j], 0, 0, 0);
+        }
+        // Step-0 reads first, then step 1's reads spread over step 0's MFMAs.
+        __builtin_amdgcn_sched_group_barrier(0x100, NR, 0);
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+          __builtin_amdgcn_sched_group_barrier(0x008, NM / NR > 0 ? NM / NR : 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, NM - (NM / NR > 0 ? NM / NR : 1) * NR, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, NM, 0);
+      }
+      // All waves are done reading both stages before the next tile's first load.
+      __builtin_amdgcn_s_barrier();
+    }
+    const int m_base = row0_a + wm * TM;
+    const int n_base = row0_b + (PAIRED ? wn * (TN / 2) : wn * TN);
+    Epi::run(p, acc, m_base, n_base, lane, tm, tn, wn);
+  }
+}
+
+}  // namespace ws

@@ -4,7 +4,7 @@
 #include <stdarg.h>
 #include <stdio.h>
 
-#include "gemm.h"
+#include "gemm_fast.h"
 
 namespace ws {
 
@@ -110,5 +110,50 @@ int dispatch(const GemmParams& p, int am, int bm, LaunchCfg cfg, hipStream_t s) 
 }
 
 inline bool fits_i32(long v) { return v >= 0 && v < 0x7fffffffL; }
+
+// Fast path (gemm_fast.h): 256 x 256 tiles, direct-to-LDS loads, 16x16x32 MFMA.
+template <int AM, int BMD, bool PAIRED, class Epi>
+int run_fast(GemmParams p, LaunchCfg cfg, hipStream_t stream) {
+  const void* kern = reinterpret_cast<const void*>(&gemm_fast_kernel<AM, BMD, PAIRED, Epi>);
+  if (int rc = ensure_lds(kern, kFLdsBytes)) return rc;
+  const int cols = PAIRED ? p.H : p.N;
+  const int bn_cols = PAIRED ? kFBN / 2 : kFBN;
+  p.tiles_m = cdiv(p.M, kFBM);
+  p.tiles_n = cdiv(cols, bn_cols);
+  p.total_tiles = p.tiles_m * p.tiles_n;
+  const int k_tiles = cdiv(p.K, kFBK);
+  const int splits = cfg.splits < 1 ? 1 : cfg.splits;
+  p.k_tiles_per_split = cdiv(k_tiles, splits);
+  if (p.k_tiles_per_split < 1) p.k_tiles_per_split = 1;
+  const int resident = device_cus();
+  dim3 grid(cfg.persistent ? (p.total_tiles < resident ? p.total_tiles : resident) : p.total_tiles,
+            splits);
+  hipLaunchKernelGGL((gemm_fast_kernel<AM, BMD, PAIRED, Epi>), grid, dim3(kFNT), kFLdsBytes, stream, p);
+  return hip_check(hipGetLastError(), "gemm launch");
+}
+
+// True when both operand modes can take the fast path for a 256-row tile. The vector
+// modes already guarantee 16-byte aligned chunks and whole-chunk edges; the per-tile
+// 32-bit offsets are bounded here (paired B tiles reach `half` rows further).
+inline bool fast_ok(const GemmParams& p, int am, int bm, bool paired) {
+  if (am == kGeneric || bm == kGeneric) return false;
+  const long lim = 0x7fffffffL;
+  const long half = paired ? p.H : 0;
+  if (am == kKContig && (256L + 1) * p.a.s_row * 2 >= lim) return false;
+  if (am == kMNContig && 2L * 256 + 64L * p.a.s_k * 2 >= lim) return false;
+  if (bm == kKContig && (256L + half + 1) * p.b.s_row * 2 >= lim) return false;
+  if (bm == kMNContig && 2L * (256 + half) + 64L * p.b.s_k * 2 >= lim) return false;
+  return true;
+}
+
+template <bool PAIRED, class Epi>
+int dispatch_fast(const GemmParams& p, int am, int bm, LaunchCfg cfg, hipStream_t s) {
+  switch (am * 2 + bm) {
+    case 0: return run_fast<kKContig, kKContig, PAIRED, Epi>(p, cfg, s);
+    case 1: return run_fast<kKContig, kMNContig, PAIRED, Epi>(p, cfg, s);
+    case 2: return run_fast<kMNContig, kKContig, PAIRED, Epi>(p, cfg, s);
+    default: return run_fast<kMNContig, kMNContig, PAIRED, Epi>(p, cfg, s);
+  }
+}
 
 }  // namespace ws

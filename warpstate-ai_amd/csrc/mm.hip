@@ -50,6 +50,8 @@ extern "C" int ws_mm(const void* a, int64_t a_s0, int64_t a_s1, const void* b, i
   const int am = operand_mode(p.a, m, k, rows), bm = operand_mode(p.b, n, k, rows);
   LaunchCfg cfg{algorithm != 0, 1};
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (tile == kTileLarge && fast_ok(p, am, bm, false))
+    return dispatch_fast<false, FEpiStore<false, false>>(p, am, bm, cfg, s);
   if (tile == kTileLarge)
     return dispatch<kMaskMM, WS_TILE_ARGS_LARGE, false, false, EpiStore<false, false>>(p, am, bm, cfg, s);
   return dispatch<kMaskMM, WS_TILE_ARGS_SMALL, false, false, EpiStore<false, false>>(p, am, bm, cfg, s);
@@ -83,6 +85,8 @@ extern "C" int ws_swiglu_mm(const void* a, int64_t a_s0, int64_t a_s1, const voi
   if (bm == kMNContig && 2L * (h + rows) >= 0x7fffffffL) bm = kGeneric;
   LaunchCfg cfg{algorithm != 0, 1};
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (tile == kTileLarge && fast_ok(p, am, bm, true))
+    return dispatch_fast<true, FEpiSwiglu>(p, am, bm, cfg, s);
   if (tile == kTileLarge)
     return dispatch<kMaskKK | kMaskGG, WS_TILE_ARGS_LARGE, true, false, EpiSwiglu>(p, am, bm, cfg, s);
   return dispatch<kMaskKK | kMaskGG, WS_TILE_ARGS_SMALL, true, false, EpiSwiglu>(p, am, bm, cfg, s);

@@ -39,6 +39,61 @@ static __global__ void __launch_bounds__(256) rms_rstd_kernel(const unsigned sho
   if (lane == 0) rstd[row] = 1.0f / sqrtf(acc / (float)D + eps);
 }
 
+// RMSNorm of x (row stride ldx) into a contiguous BF16 y with the eager rounding of
+// RMSNorm.forward (warpstate/model.py:25-28): y = r(r(x * rstd) * r(w)); also stores
+// rstd. One wave per row; with `vec`, 16-byte loads and stores of 8 elements per lane.
+// The GEMM prologue of the fused input projection.
+static __global__ void __launch_bounds__(256) rmsnorm_rows_kernel(
+    const unsigned short* __restrict__ x, long ldx, const float* __restrict__ w,
+    unsigned short* __restrict__ y, float* __restrict__ rstd, int rows, int D, float eps,
+    int vec) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const unsigned short* xr = x + (long)row * ldx;
+  unsigned short* yr = y + (long)row * D;
+  float acc = 0.0f;
+  if (vec) {
+    for (int c = lane * 8; c < D; c += 64 * 8) {
+      const u32x4_t v = *reinterpret_cast<const u32x4_t*>(xr + c);
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        const float a = lo_bf16(v[d]), b = hi_bf16(v[d]);
+        acc += a * a;
+        acc += b * b;
+      }
+    }
+  } else {
+    for (int c = lane; c < D; c += 64) {
+      const float a = bf16_bits_to_f32(xr[c]);
+      acc += a * a;
+    }
+  }
+  acc = wave_sum(acc);
+  const float r = 1.0f / sqrtf(acc / (float)D + eps);
+  if (vec) {
+    for (int c = lane * 8; c < D; c += 64 * 8) {
+      const u32x4_t v = *reinterpret_cast<const u32x4_t*>(xr + c);
+      const f32x4_t w0 = *reinterpret_cast<const f32x4_t*>(w + c);
+      const f32x4_t w1 = *reinterpret_cast<const f32x4_t*>(w + c + 4);
+      const float wv[8] = {w0[0], w0[1], w0[2], w0[3], w1[0], w1[1], w1[2], w1[3]};
+      u32x4_t o;
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        const float z0 = rbf16(lo_bf16(v[d]) * r), z1 = rbf16(hi_bf16(v[d]) * r);
+        o[d] = pack_bf16x2(z0 * rbf16(wv[2 * d]), z1 * rbf16(wv[2 * d + 1]));
+      }
+      *reinterpret_cast<u32x4_t*>(yr + c) = o;
+    }
+  } else {
+    for (int c = lane; c < D; c += 64) {
+      const float z = rbf16(bf16_bits_to_f32(xr[c]) * r);
+      yr[c] = to_bf16_bits(z * rbf16(w[c]));
+    }
+  }
+  if (lane == 0) rstd[row] = r;
+}
+
 // Standalone BF16 RMSNorm forward (ops/activation_execution.py:96-110): z = x * rstd,
 // y = z * w with z and w rounded to BF16 when eager; also stores rstd.
 static __global__ void __launch_bounds__(256) rmsnorm_fwd_kernel(const unsigned short* __restrict__ x,

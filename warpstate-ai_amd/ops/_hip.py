@@ -37,8 +37,9 @@ SIGNATURES = {
     "ws_rmsnorm_backward": (_i32, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                                    _c_void_p, _c_void_p, _i64, _i64, _i32, _c_void_p]),
     "ws_rms_rstd": (_i32, [_c_void_p, _i64, _c_void_p, _i64, _i64, _f32, _c_void_p]),
-    "ws_rmsnorm_gate_mm": (_i32, [_c_void_p, _i64, _c_void_p, _f32, _c_void_p, _c_void_p, _i64,
-                                  _i64, _c_void_p, _i64, _i64, _i64, _i64, _i64, _c_void_p]),
+    "ws_rmsnorm_gate_mm": (_i32, [_c_void_p, _i64, _c_void_p, _f32, _c_void_p, _c_void_p,
+                                  _c_void_p, _i64, _i64, _c_void_p, _i64, _i64, _i64, _i64,
+                                  _i64, _c_void_p]),
     "ws_residual_mm": (_i32, [_c_void_p, _i64, _i64, _c_void_p, _i64, _i64, _c_void_p, _i64,
                               _c_void_p, _i64, _i64, _i64, _c_void_p]),
     "ws_swiglu_backward_mm": (_i32, [_c_void_p, _i64, _i64, _c_void_p, _i64, _i64, _c_void_p,
@@ -50,9 +51,10 @@ SIGNATURES = {
     "ws_linear_ce_forward": (_i32, [_c_void_p, _i64, _c_void_p, _i64, _c_void_p, _i64, _i64, _i64,
                                     _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                                     _c_void_p, _c_void_p, _c_void_p]),
+    "ws_linear_ce_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64]),
     "ws_linear_ce_backward": (_i32, [_c_void_p, _i64, _c_void_p, _i64, _c_void_p, _c_void_p,
                                      _c_void_p, _c_void_p, _i64, _i64, _i64, _c_void_p, _i64,
-                                     _c_void_p, _c_void_p, _i64, _c_void_p]),
+                                     _c_void_p, _i64, _c_void_p]),
 }
 
 _lock = threading.Lock()

@@ -24,7 +24,7 @@ import torch
 
 from ops import _hip
 
-DEFAULT_CE_CHUNK_ROWS = 2048
+DEFAULT_CE_CHUNK_ROWS = 4096
 
 
 def _check_bf16_cuda(*tensors):
@@ -49,12 +49,15 @@ def mm(a: torch.Tensor, b: torch.Tensor, algorithm: str = "tiled", tile: int = 0
 
 def rmsnorm_gate_mm(x: torch.Tensor, norm_weight: torch.Tensor, eps: float,
                     weight: torch.Tensor, gate: tuple[int, int] = (0, 0),
-                    out: torch.Tensor | None = None, rstd: torch.Tensor | None = None
+                    out: torch.Tensor | None = None, rstd: torch.Tensor | None = None,
+                    normed: torch.Tensor | None = None
                     ) -> tuple[torch.Tensor, torch.Tensor]:
     """``(r(RMSNorm(x) @ weight.T) with sigmoid on columns [gate), rstd)``.
 
     x [M, K] BF16 with unit column stride; norm_weight [K] FP32; weight [N, K] BF16 in
     nn.Linear layout; gate = (begin, end) output columns that get r(sigmoid(.)).
+    ``normed`` [M, K] BF16 receives the normalized operand RMSNorm(x) (the saved input of
+    the projection's weight gradient); it is allocated when not given.
     """
     _check_bf16_cuda(x, weight)
     if x.ndim != 2 or weight.ndim != 2 or x.shape[1] != weight.shape[1]:
@@ -69,10 +72,14 @@ def rmsnorm_gate_mm(x: torch.Tensor, norm_weight: torch.Tensor, eps: float,
         out = torch.empty((m, n), dtype=torch.bfloat16, device=x.device)
     if rstd is None:
         rstd = torch.empty((m,), dtype=torch.float32, device=x.device)
+    if normed is None:
+        normed = torch.empty((m, k), dtype=torch.bfloat16, device=x.device)
+    elif normed.shape != (m, k) or not normed.is_contiguous() or normed.dtype != torch.bfloat16:
+        raise ValueError("normed must be a contiguous BF16 [M, K] tensor")
     b = weight.T
     _hip.call("ws_rmsnorm_gate_mm", x.data_ptr(), x.stride(0), norm_weight.data_ptr(),
-              float(eps), rstd.data_ptr(), b.data_ptr(), b.stride(0), b.stride(1),
-              out.data_ptr(), m, n, k, int(gate[0]), int(gate[1]), _hip.stream(x))
+              float(eps), rstd.data_ptr(), normed.data_ptr(), b.data_ptr(), b.stride(0),
+              b.stride(1), out.data_ptr(), m, n, k, int(gate[0]), int(gate[1]), _hip.stream(x))
     return out, rstd
 
 
@@ -137,7 +144,7 @@ def mm_accumulate_(g: torch.Tensor, a: torch.Tensor, b: torch.Tensor, round_bf16
 class CrossEntropyState:
     """Per-call buffers of the fused LM-head cross-entropy."""
 
-    def __init__(self, rows, vocab, device, chunk_rows=DEFAULT_CE_CHUNK_ROWS):
+    def __init__(self, rows, vocab, device, chunk_rows=DEFAULT_CE_CHUNK_ROWS, d=None):
         parts = _hip.query("ws_linear_ce_parts", vocab)
         f32 = dict(dtype=torch.float32, device=device)
         self.part_max = torch.empty((rows, parts), **f32)
@@ -147,10 +154,20 @@ class CrossEntropyState:
         self.loss = torch.empty((rows,), **f32)
         self.mean = torch.empty((), **f32)
         self.count = torch.empty((), **f32)
-        self.scale = torch.empty((1,), **f32)
+        self.rows, self.vocab = rows, vocab
         self.chunk_rows = min(chunk_rows, rows)
-        self.grad_logits = torch.empty((self.chunk_rows, vocab), dtype=torch.bfloat16,
-                                       device=device)
+        self.workspace = None
+        if d is not None:
+            self.backward_workspace(d)
+
+    def backward_workspace(self, d):
+        """The backward's workspace (scale, one chunk of BF16 logit gradients, split-K
+        partials), allocated once per hidden width; 256-byte aligned by the allocator."""
+        need = _hip.query("ws_linear_ce_workspace_bytes", self.rows, self.vocab, d,
+                          self.chunk_rows)
+        if self.workspace is None or self.workspace.numel() < need:
+            self.workspace = torch.empty((need,), dtype=torch.uint8, device=self.lse.device)
+        return self.workspace
 
 
 def _check_ce(hidden, weight, targets):
@@ -192,11 +209,11 @@ def linear_cross_entropy_backward(hidden: torch.Tensor, weight: torch.Tensor,
     grad_mean = grad_mean.reshape(1).to(torch.float32).contiguous()
     if out is None:
         out = torch.empty((rows, d), dtype=torch.bfloat16, device=hidden.device)
+    workspace = state.backward_workspace(d)
     _hip.call("ws_linear_ce_backward", hidden.data_ptr(), hidden.stride(0), weight.data_ptr(),
               weight.stride(0), targets.data_ptr(), state.lse.data_ptr(), state.count.data_ptr(),
-              grad_mean.data_ptr(), rows, vocab, d, state.grad_logits.data_ptr(),
-              state.chunk_rows, state.scale.data_ptr(), out.data_ptr(), out.stride(0),
-              _hip.stream(hidden))
+              grad_mean.data_ptr(), rows, vocab, d, workspace.data_ptr(), state.chunk_rows,
+              out.data_ptr(), out.stride(0), _hip.stream(hidden))
     return out
 
 
