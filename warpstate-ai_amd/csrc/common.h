@@ -56,10 +56,14 @@ __device__ __forceinline__ float exp_e(float x) { return __builtin_amdgcn_exp2f(
 // Natural log through the hardware log2.
 __device__ __forceinline__ float log_e(float x) { return __builtin_amdgcn_logf(x) * kLn2; }
 
-// SiLU exactly as the reference writes it: g / (1 + e^-g) (ops/matmul_epilogue.py:80).
-__device__ __forceinline__ float silu(float g) { return g / (1.0f + exp_e(-g)); }
-// Logistic sigmoid 1 / (1 + e^-x) (ops/activation_execution.py:45).
-__device__ __forceinline__ float sigmoid(float x) { return 1.0f / (1.0f + exp_e(-x)); }
+// Logistic sigmoid 1 / (1 + e^-x) (ops/activation_execution.py:45) with the hardware
+// reciprocal v_rcp_f32 (1 ulp) in place of an IEEE division; the difference is far below
+// the BF16 rounding every result of it goes through.
+__device__ __forceinline__ float sigmoid(float x) {
+  return __builtin_amdgcn_rcpf(1.0f + exp_e(-x));
+}
+// SiLU g / (1 + e^-g) (ops/matmul_epilogue.py:80), as g times that reciprocal.
+__device__ __forceinline__ float silu(float g) { return g * sigmoid(g); }
 
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

@@ -119,12 +119,29 @@ def swiglu_backward_mm(grad: torch.Tensor, down_weight: torch.Tensor, packed: to
     return out
 
 
+def auto_splits(m: int, n: int, k: int, cus: int = 256, tile: int = 256,
+                max_splits: int = 4, min_k_tiles: int = 16) -> int:
+    """Split-K factor for an [m, n] output with reduction k: the one (fewest on ties) that
+    fills the last round of 256 x 256 tiles on `cus` compute units best, keeping at least
+    `min_k_tiles` 64-wide k-tiles per split."""
+    tiles = -(-m // tile) * -(-n // tile)
+    best, best_eff = 1, 0.0
+    for s in range(1, max_splits + 1):
+        if s > 1 and -(-k // 64) // s < min_k_tiles:
+            break
+        work = tiles * s
+        eff = work / (-(-work // cus) * cus)
+        if eff > best_eff + 1e-9:
+            best, best_eff = s, eff
+    return best
+
+
 def mm_accumulate_(g: torch.Tensor, a: torch.Tensor, b: torch.Tensor, round_bf16: bool = True,
-                   splits: int = 1, workspace: torch.Tensor | None = None) -> torch.Tensor:
+                   splits: int | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
     """G += f32(r(a @ b)) (or G += a @ b in FP32 when ``round_bf16`` is False), in place.
 
     G is FP32 [M, N] with unit column stride; ``splits`` > 1 splits the reduction through
-    an FP32 workspace of splits * M * N floats."""
+    an FP32 workspace of splits * M * N floats (None: chosen by ``auto_splits``)."""
     _check_bf16_cuda(a, b)
     if g.dtype != torch.float32 or g.stride(1) != 1:
         raise ValueError("Gradient buffer must be FP32 with unit column stride")
@@ -132,6 +149,8 @@ def mm_accumulate_(g: torch.Tensor, a: torch.Tensor, b: torch.Tensor, round_bf16
     n = b.shape[1]
     if g.shape != (m, n) or b.shape[0] != k:
         raise ValueError("Gradient buffer shape must match a @ b")
+    if splits is None:
+        splits = auto_splits(m, n, k, torch.cuda.get_device_properties(g.device).multi_processor_count)
     need = _hip.query("ws_mm_accumulate_workspace_floats", m, n, splits)
     if need and (workspace is None or workspace.numel() < need):
         workspace = torch.empty((need,), dtype=torch.float32, device=g.device)
@@ -245,7 +264,7 @@ def linear_cross_entropy(hidden, weight, targets):
 def mlp_backward(x: torch.Tensor, w_upgate: torch.Tensor, w_down: torch.Tensor,
                  packed: torch.Tensor, act: torch.Tensor, dy: torch.Tensor,
                  g_upgate: torch.Tensor, g_down: torch.Tensor, eager_rounding: bool = True,
-                 dw_splits: int = 1) -> torch.Tensor:
+                 dw_splits: int | None = None) -> torch.Tensor:
     """Backward of y = down(silu(gate) * up) with (up | gate) = x @ w_upgate.T.
 
     x [M, d], w_upgate [2H, d], w_down [d, H] (nn.Linear layouts, BF16), packed [M, 2H] and
