@@ -80,6 +80,13 @@ int ws_rmsnorm_backward(const void* x, const float* weight, const float* rstd, c
                         void* dx, float* dweight, float* partial, int64_t rows, int64_t d,
                         int eager_rounding, void* stream);
 
+/* out[cols, rows] = transpose(in[rows, cols]) for BF16 (in has row stride ld_in, out is
+ * contiguous). Used to give weight-side GEMM operands a contiguous reduction dimension:
+ * the input gradient dX = dY @ W (ops/matmul_execution.py:239) then reads W^T rows.
+ * No reference counterpart (a layout step of this implementation). */
+int ws_transpose_bf16(const void* in, int64_t ld_in, void* out, int64_t rows, int64_t cols,
+                      void* stream);
+
 /* Row statistics of RMSNorm: rstd[r] = 1/sqrt(mean_k f32(x[r,k])^2 + eps) for x with row
  * stride ldx (warpstate/model.py:26-27). */
 int ws_rms_rstd(const void* x, int64_t ldx, float* rstd, int64_t rows, int64_t d, float eps,
@@ -157,10 +164,13 @@ int64_t ws_linear_ce_workspace_bytes(int64_t rows, int64_t vocab, int64_t d, int
  * chunk_rows at a time: the BF16 logit gradients of one chunk ([chunk_rows, vocab], never
  * the whole batch) go to the 256-byte aligned `workspace` and feed that chunk's dHidden
  * GEMM, split over the vocab with FP32 partials when the chunk alone would not fill the
- * GPU. Restates autograd of warpstate/model.py:321-334.
+ * GPU. `weight_t` (nullable) is the head weight transposed, [d, vocab] contiguous; when
+ * given, the dHidden GEMM reads it instead of `weight`. Restates autograd of
+ * warpstate/model.py:321-334.
  */
 int ws_linear_ce_backward(const void* hidden, int64_t ld_hidden, const void* weight,
-                          int64_t ld_weight, const int64_t* targets, const float* lse,
+                          int64_t ld_weight, const void* weight_t, const int64_t* targets,
+                          const float* lse,
                           const float* count, const float* grad_mean, int64_t rows,
                           int64_t vocab, int64_t d, void* workspace, int64_t chunk_rows,
                           void* dhidden, int64_t ld_dhidden, void* stream);

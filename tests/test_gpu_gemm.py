@@ -98,3 +98,35 @@ def test_exact_small_integer_products():
             outt = launch_mm(a.T.contiguous().cuda().T, b.T.contiguous().cuda().T, "tiled", tile)
             torch.cuda.synchronize()
             assert torch.equal(outt.cpu(), exact), (m, n, k, tile, "transposed")
+
+
+@pytest.mark.parametrize("shape,stride_pad", [((64, 64), 0), ((1000, 2056), 8), ((37, 91), 5),
+                                              ((2048, 11264), 0)])
+def test_transpose_is_bit_exact(shape, stride_pad):
+    """The weight-layout transpose used by the input-gradient GEMMs moves bits only."""
+    from ops.fused_execution import transpose
+
+    rows, cols = shape
+    gen = torch.Generator("cpu").manual_seed(21)
+    full = torch.randn(rows, cols + stride_pad, generator=gen).bfloat16().cuda()
+    x = full[:, :cols]
+    out = transpose(x)
+    torch.cuda.synchronize()
+    assert out.shape == (cols, rows) and out.is_contiguous()
+    assert torch.equal(out.cpu(), x.cpu().T.contiguous())
+
+
+def test_input_gradient_layout_uses_transposed_weight_and_matches():
+    """dX = dY @ W with W N-contiguous and many rows takes the transposed-weight path; the
+    result must match the oracle as any other layout does."""
+    from ops.fused_execution import k_contiguous_b
+    from ops.matmul_kernels import launch_mm
+
+    gen = torch.Generator("cpu").manual_seed(8)
+    dy = torch.randn(2048, 640, generator=gen).bfloat16()
+    w = (torch.randn(640, 384, generator=gen) * 0.05).bfloat16()
+    gdy, gw = dy.cuda(), w.cuda()
+    assert k_contiguous_b(gw, 2048).stride() == (1, 640)
+    out = launch_mm(gdy, gw, "tiled", (128, 128, 32, 4, 3))
+    torch.cuda.synchronize()
+    assert_bf16_close(out, oracle.mm(dy, w), "dX with transposed weight")

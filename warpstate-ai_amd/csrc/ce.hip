@@ -47,6 +47,7 @@ extern "C" int ws_linear_ce_forward(const void* hidden, int64_t ld_hidden, const
   p.part_sum = part_sum;
   p.tgt_logit = target_logit;
   p.parts_per_row = (int)ws_linear_ce_parts(vocab);
+  p.vec_out = 1;  // the statistics epilogue stores no output tile
   int am = operand_mode(p.a, rows, d, 256), bm = operand_mode(p.b, vocab, d, 256);
   if (fast_ok(p, am, bm, false)) {
     if (int rc = dispatch_fast<false, FEpiCEStats>(p, am, bm, LaunchCfg{0, 1}, s)) return rc;
@@ -85,7 +86,8 @@ extern "C" int64_t ws_linear_ce_workspace_bytes(int64_t rows, int64_t vocab, int
 }
 
 extern "C" int ws_linear_ce_backward(const void* hidden, int64_t ld_hidden, const void* weight,
-                                     int64_t ld_weight, const int64_t* targets, const float* lse,
+                                     int64_t ld_weight, const void* weight_t,
+                                     const int64_t* targets, const float* lse,
                                      const float* count, const float* grad_mean, int64_t rows,
                                      int64_t vocab, int64_t d, void* workspace,
                                      int64_t chunk_rows, void* dhidden, int64_t ld_dhidden,
@@ -127,10 +129,13 @@ extern "C" int ws_linear_ce_backward(const void* hidden, int64_t ld_hidden, cons
     // dHidden of the chunk: r(G [r, vocab] @ W [vocab, d]), split over the vocab.
     GemmParams q{};
     q.a = OperandDesc{gl, vocab, 1};
-    q.b = OperandDesc{static_cast<const unsigned short*>(weight), 1, ld_weight};
+    // B [vocab, d]: the head weight (d contiguous) or its transpose (vocab contiguous).
+    q.b = weight_t ? OperandDesc{static_cast<const unsigned short*>(weight_t), vocab, 1}
+                   : OperandDesc{static_cast<const unsigned short*>(weight), 1, ld_weight};
     q.M = (int)r; q.N = (int)d; q.K = (int)vocab;
     unsigned short* out = static_cast<unsigned short*>(dhidden) + start * ld_dhidden;
     int qa = operand_mode(q.a, r, vocab, 256), qb = operand_mode(q.b, d, vocab, 256);
+    q.vec_out = (d % 4 == 0) && (ld_dhidden % 4 == 0) && (reinterpret_cast<unsigned long>(out) % 8 == 0);
     const bool fast = fast_ok(q, qa, qb, false);
     if (splits > 1 && fast) {
       q.g = partials;

@@ -109,7 +109,8 @@ extern "C" int ws_swiglu_backward_mm(const void* grad, int64_t g_s0, int64_t g_s
   p.aux = static_cast<const unsigned short*>(packed);
   p.ldaux = 2 * h;
   p.eager = eager_rounding ? 1 : 0;
-  p.vec_out = (h % 4 == 0) && al(dpacked, 8) && al(packed, 8);
+  // The staged fast epilogue moves 8 columns per lane.
+  p.vec_out = (h % 8 == 0) && al(dpacked, 16) && al(packed, 16);
   int am = operand_mode(p.a, m, k, 256), bm = operand_mode(p.b, h, k, 256);
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (fast_ok(p, am, bm, false))

@@ -40,6 +40,11 @@ constexpr int kFNT = kFWM * kFWN * kWave;               // 512 threads
 constexpr int kFTileBytes = 256 * kFBK * 2;             // one operand tile, 32 KiB
 constexpr int kFStageBytes = 2 * kFTileBytes;
 constexpr int kFLdsBytes = 2 * kFStageBytes;            // 128 KiB
+// Epilogue staging: each wave's 64 x 128 BF16 tile, rows padded to 272 bytes so that both
+// the fragment-order writes and the row-order 16-byte reads are bank-conflict free.
+constexpr int kFStageRow = 272;
+constexpr int kFStageWave = 64 * kFStageRow;
+constexpr int kFLdsAlloc = 8 * kFStageWave > kFLdsBytes ? 8 * kFStageWave : kFLdsBytes;
 constexpr int kFIns = kFTileBytes / (kFNT * 16);         // 4 loads per thread per operand
 
 typedef float f32x4_v __attribute__((ext_vector_type(4)));
@@ -134,6 +139,8 @@ struct Acc16 {
 // --------------------------------------------------------------------------------------
 // Epilogues on the 16x16 accumulator layout. Lane l holds, for block (i, j), row
 //   m = m_base + 16 i + (l & 15) and columns n = n_base + 16 j + 4 (l >> 4) + e.
+// They store whole 4-column vectors only (GemmParams::vec_out); the host sends shapes
+// without vector outputs to the generic kernel of gemm.h.
 
 // Plain BF16 store with optional column-range sigmoid and BF16 residual add
 // (same numerics as EpiStore).
@@ -141,7 +148,8 @@ template <bool SIGMOID, bool RESIDUAL>
 struct FEpiStore {
   template <int FA, int FB>
   __device__ __forceinline__ static void run(const GemmParams& p, Acc16<FA, FB>& acc, int m_base,
-                                             int n_base, int lane, int tm, int tn, int wn) {
+                                             int n_base, int lane, int tm, int tn, int wn,
+                                             unsigned char* stage) {
     const int m0 = tm * kFBM, n0 = tn * kFBN;
     unsigned short* cbase = p.c + (long)m0 * p.ldc + n0;
     __amdgpu_buffer_rsrc_t rc = make_rsrc(cbase, 0x7fffffff);
@@ -164,7 +172,7 @@ struct FEpiStore {
           }
           v[e] = x;
         }
-        if (p.vec_out) {
+        {
           const bool ok = mok && (n + 3 < p.N);
           if (RESIDUAL) {
             u32x2_t rv = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(
@@ -177,14 +185,6 @@ struct FEpiStore {
           u32x2_t out = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
           __builtin_amdgcn_raw_buffer_store_b64(out, rc,
                                                 store_off(ok, (long)(m - m0) * p.ldc + (n - n0), 2), 0, 0);
-        } else {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const bool ok = mok && (n + e < p.N);
-            float x = v[e];
-            if (RESIDUAL && ok) x = rbf16(x) + bf16_bits_to_f32(rbase[(long)(m - m0) * p.ldaux + (n + e - n0)]);
-            if (ok) cbase[(long)(m - m0) * p.ldc + (n + e - n0)] = to_bf16_bits(x);
-          }
         }
       }
     }
@@ -196,7 +196,8 @@ struct FEpiStore {
 struct FEpiSwiglu {
   template <int FA, int FB>
   __device__ __forceinline__ static void run(const GemmParams& p, Acc16<FA, FB>& acc, int m_base,
-                                             int n_base, int lane, int tm, int tn, int wn) {
+                                             int n_base, int lane, int tm, int tn, int wn,
+                                             unsigned char* stage) {
     constexpr int FH = FB / 2;
     const int m0 = tm * kFBM, n0 = tn * (kFBN / 2);
     unsigned short* pbase = p.c + (long)m0 * p.ldc + n0;
@@ -220,7 +221,7 @@ struct FEpiSwiglu {
           if (p.eager) s = rbf16(s);
           act[e] = s * up[e];
         }
-        if (p.vec_out) {
+        {
           const bool ok = mok && (n + 3 < p.H);
           const long rowp = (long)(m - m0) * p.ldc + (n - n0);
           u32x2_t vu = {pack_bf16x2(up[0], up[1]), pack_bf16x2(up[2], up[3])};
@@ -230,87 +231,84 @@ struct FEpiSwiglu {
           __builtin_amdgcn_raw_buffer_store_b64(vg, rp, store_off(ok, rowp + hoff, 2), 0, 0);
           __builtin_amdgcn_raw_buffer_store_b64(
               va, ra, store_off(ok, (long)(m - m0) * p.ldc2 + (n - n0), 2), 0, 0);
-        } else {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            if (mok && n + e < p.H) {
-              const long rowp = (long)(m - m0) * p.ldc + (n + e - n0);
-              pbase[rowp] = to_bf16_bits(up[e]);
-              pbase[rowp + hoff] = to_bf16_bits(gate[e]);
-              abase[(long)(m - m0) * p.ldc2 + (n + e - n0)] = to_bf16_bits(act[e]);
-            }
-          }
         }
       }
     }
   }
 };
 
-// SwiGLU backward on the dAct GEMM (EpiSwigluBwd numerics).
+// SwiGLU backward on the dAct GEMM (EpiSwigluBwd numerics). With vector outputs the
+// rounded dAct tile goes through this wave's LDS staging region so that the saved packed
+// projection is read, and dPacked written, as 16-byte row-contiguous pieces (8 columns
+// per lane, 16 lanes per 128-column row, 4 rows per instruction, 16 rows in flight).
 struct FEpiSwigluBwd {
+  __device__ __forceinline__ static void math(const GemmParams& p, float dy, float up, float gate,
+                                              float& du, float& dg) {
+    const float sg = sigmoid(gate);
+    float s = gate * sg;
+    if (p.eager) s = rbf16(s);
+    float dsilu = dy * up;
+    if (p.eager) dsilu = rbf16(dsilu);
+    du = dy * s;
+    dg = (dsilu * sg) * (1.0f + gate * (1.0f - sg));
+  }
   template <int FA, int FB>
   __device__ __forceinline__ static void run(const GemmParams& p, Acc16<FA, FB>& acc, int m_base,
-                                             int n_base, int lane, int tm, int tn, int wn) {
-    const int m0 = tm * kFBM, n0 = tn * kFBN;
-    unsigned short* dbase = p.c + (long)m0 * p.ldc + n0;
-    const unsigned short* pbase = p.aux + (long)m0 * p.ldaux + n0;
-    __amdgpu_buffer_rsrc_t rd = make_rsrc(dbase, 0x7fffffff);
-    __amdgpu_buffer_rsrc_t rp = make_rsrc(pbase, 0x7fffffff);
+                                             int n_base, int lane, int tm, int tn, int wn,
+                                             unsigned char* stage) {
     const long hoff = p.H;
+    {
+      // Fragment order -> staging rows (64 x 128 BF16, 272-byte rows).
 #pragma unroll
-    for (int i = 0; i < FA; ++i) {
-      const int m = m_base + 16 * i + (lane & 15);
-      const bool mok = m < p.M;
+      for (int i = 0; i < FA; ++i)
 #pragma unroll
-      for (int j = 0; j < FB; ++j) {
-        const int n = n_base + 16 * j + 4 * (lane >> 4);
-        const bool ok4 = mok && (n + 3 < p.N);
-        float up[4], gate[4];
-        if (p.vec_out) {
-          const long rowp = (long)(m - m0) * p.ldaux + (n - n0);
-          u32x2_t vu = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(
-              rp, store_off(ok4, rowp, 2), 0, 0));
-          u32x2_t vg = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(
-              rp, store_off(ok4, rowp + hoff, 2), 0, 0));
-          up[0] = lo_bf16(vu[0]); up[1] = hi_bf16(vu[0]); up[2] = lo_bf16(vu[1]); up[3] = hi_bf16(vu[1]);
-          gate[0] = lo_bf16(vg[0]); gate[1] = hi_bf16(vg[0]); gate[2] = lo_bf16(vg[1]); gate[3] = hi_bf16(vg[1]);
-        } else {
+        for (int j = 0; j < FB; ++j) {
+          const int r = 16 * i + (lane & 15), c = 16 * j + 4 * (lane >> 4);
+          u32x2_t v = {pack_bf16x2(acc.v[i][j][0], acc.v[i][j][1]),
+                       pack_bf16x2(acc.v[i][j][2], acc.v[i][j][3])};
+          *reinterpret_cast<u32x2_t*>(stage + r * kFStageRow + c * 2) = v;
+        }
+      // Keep the scheduler from hoisting the loads below above the staging writes (the
+      // accumulators must be dead before the loaded rows take their registers).
+      __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's staging writes landed
+      const int c8 = 8 * (lane & 15);       // this lane's 8 columns
+      const int n = n_base + c8;
+      // Buffer bases at this wave's tile origin keep the byte offsets small.
+      __amdgpu_buffer_rsrc_t rp = make_rsrc(p.aux + (long)m_base * p.ldaux + n_base, 0x7fffffff);
+      __amdgpu_buffer_rsrc_t rd = make_rsrc(p.c + (long)m_base * p.ldc + n_base, 0x7fffffff);
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const bool ok = mok && (n + e < p.N);
-            const long rowp = (long)(m - m0) * p.ldaux + (n + e - n0);
-            up[e] = ok ? bf16_bits_to_f32(pbase[rowp]) : 0.0f;
-            gate[e] = ok ? bf16_bits_to_f32(pbase[rowp + hoff]) : 0.0f;
+      for (int q = 0; q < 4; ++q) {
+        u32x4_t vu[4], vg[4];
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+          const int r = 16 * q + 4 * h + (lane >> 4);
+          const int m = m_base + r;
+          const bool ok = m < p.M && n + 7 < p.N;
+          const long off = (long)r * p.ldaux + c8;
+          vu[h] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rp, store_off(ok, off, 2), 0, 0));
+          vg[h] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rp, store_off(ok, off + hoff, 2), 0, 0));
+        }
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+          const int r = 16 * q + 4 * h + (lane >> 4);
+          const int m = m_base + r;
+          const bool ok = m < p.M && n + 7 < p.N;
+          const u32x4_t vd = *reinterpret_cast<const u32x4_t*>(stage + r * kFStageRow + c8 * 2);
+          u32x4_t od, og;
+#pragma unroll
+          for (int d = 0; d < 4; ++d) {
+            float du0, dg0, du1, dg1;
+            math(p, lo_bf16(vd[d]), lo_bf16(vu[h][d]), lo_bf16(vg[h][d]), du0, dg0);
+            math(p, hi_bf16(vd[d]), hi_bf16(vu[h][d]), hi_bf16(vg[h][d]), du1, dg1);
+            od[d] = pack_bf16x2(du0, du1);
+            og[d] = pack_bf16x2(dg0, dg1);
           }
+          const long off = (long)r * p.ldc + c8;
+          __builtin_amdgcn_raw_buffer_store_b128(od, rd, store_off(ok, off, 2), 0, 0);
+          __builtin_amdgcn_raw_buffer_store_b128(og, rd, store_off(ok, off + hoff, 2), 0, 0);
         }
-        float du[4], dg[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float dy = rbf16(acc.v[i][j][e]);
-          const float sg = sigmoid(gate[e]);
-          float s = silu(gate[e]);
-          if (p.eager) s = rbf16(s);
-          float dsilu = dy * up[e];
-          if (p.eager) dsilu = rbf16(dsilu);
-          du[e] = dy * s;
-          dg[e] = (dsilu * sg) * (1.0f + gate[e] * (1.0f - sg));
-        }
-        if (p.vec_out) {
-          const long rowd = (long)(m - m0) * p.ldc + (n - n0);
-          u32x2_t vu = {pack_bf16x2(du[0], du[1]), pack_bf16x2(du[2], du[3])};
-          u32x2_t vg = {pack_bf16x2(dg[0], dg[1]), pack_bf16x2(dg[2], dg[3])};
-          __builtin_amdgcn_raw_buffer_store_b64(vu, rd, store_off(ok4, rowd, 2), 0, 0);
-          __builtin_amdgcn_raw_buffer_store_b64(vg, rd, store_off(ok4, rowd + hoff, 2), 0, 0);
-        } else {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            if (mok && n + e < p.N) {
-              const long rowd = (long)(m - m0) * p.ldc + (n + e - n0);
-              dbase[rowd] = to_bf16_bits(du[e]);
-              dbase[rowd + hoff] = to_bf16_bits(dg[e]);
-            }
-          }
-        }
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
   }
@@ -321,7 +319,8 @@ template <bool SPLIT>
 struct FEpiAccF32 {
   template <int FA, int FB>
   __device__ __forceinline__ static void run(const GemmParams& p, Acc16<FA, FB>& acc, int m_base,
-                                             int n_base, int lane, int tm, int tn, int wn) {
+                                             int n_base, int lane, int tm, int tn, int wn,
+                                             unsigned char* stage) {
     const int m0 = tm * kFBM, n0 = tn * kFBN;
     float* gbase = p.g + (SPLIT ? (long)blockIdx.y * p.split_stride : 0) + (long)m0 * p.ldg + n0;
     __amdgpu_buffer_rsrc_t rg = make_rsrc(gbase, 0x7fffffff);
@@ -332,7 +331,7 @@ struct FEpiAccF32 {
 #pragma unroll
       for (int j = 0; j < FB; ++j) {
         const int n = n_base + 16 * j + 4 * (lane >> 4);
-        if (p.vec_out) {
+        {
           const bool ok = mok && (n + 3 < p.N);
           const unsigned off = store_off(ok, (long)(m - m0) * p.ldg + (n - n0), 4);
           f32x4_t add;
@@ -346,16 +345,6 @@ struct FEpiAccF32 {
             add = old + add;
           }
           __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, add), rg, off, 0, 0);
-        } else {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            if (mok && n + e < p.N) {
-              const float x = acc.v[i][j][e];
-              float* dst = gbase + (long)(m - m0) * p.ldg + (n + e - n0);
-              if (SPLIT) *dst = x;
-              else *dst += p.round_acc ? rbf16(x) : x;
-            }
-          }
         }
       }
     }
@@ -368,7 +357,8 @@ struct FEpiAccF32 {
 struct FEpiCEStats {
   template <int FA, int FB>
   __device__ __forceinline__ static void run(const GemmParams& p, Acc16<FA, FB>& acc, int m_base,
-                                             int n_base, int lane, int tm, int tn, int wn) {
+                                             int n_base, int lane, int tm, int tn, int wn,
+                                             unsigned char* stage) {
     const int part = tn * kFWN + wn;
 #pragma unroll
     for (int i = 0; i < FA; ++i) {
@@ -410,7 +400,8 @@ struct FEpiCEStats {
 struct FEpiCEGrad {
   template <int FA, int FB>
   __device__ __forceinline__ static void run(const GemmParams& p, Acc16<FA, FB>& acc, int m_base,
-                                             int n_base, int lane, int tm, int tn, int wn) {
+                                             int n_base, int lane, int tm, int tn, int wn,
+                                             unsigned char* stage) {
     const int m0 = tm * kFBM, n0 = tn * kFBN;
     unsigned short* cbase = p.c + (long)m0 * p.ldc + n0;
     __amdgpu_buffer_rsrc_t rc = make_rsrc(cbase, 0x7fffffff);
@@ -430,15 +421,11 @@ struct FEpiCEGrad {
           const float l = rbf16(acc.v[i][j][e]);
           v[e] = scale * exp_e(l - lse) - ((long)(n + e) == tgt ? scale : 0.0f);
         }
-        if (p.vec_out) {
+        {
           const bool ok = mok && (n + 3 < p.N);
           u32x2_t out = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
           __builtin_amdgcn_raw_buffer_store_b64(out, rc,
                                                 store_off(ok, (long)(m - m0) * p.ldc + (n - n0), 2), 0, 0);
-        } else {
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if (mok && n + e < p.N) cbase[(long)(m - m0) * p.ldc + (n + e - n0)] = to_bf16_bits(v[e]);
         }
       }
     }
@@ -542,7 +529,9 @@ __global__ void __launch_bounds__(kFNT) gemm_fast_kernel(const GemmParams p) {
     }
     const int m_base = row0_a + wm * TM;
     const int n_base = row0_b + (PAIRED ? wn * (TN / 2) : wn * TN);
-    Epi::run(p, acc, m_base, n_base, lane, tm, tn, wn);
+    Epi::run(p, acc, m_base, n_base, lane, tm, tn, wn, fsmem + wave * kFStageWave);
+    // The next tile's loads reuse the staging space.
+    __builtin_amdgcn_s_barrier();
   }
 }
 

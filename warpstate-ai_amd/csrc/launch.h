@@ -115,7 +115,7 @@ inline bool fits_i32(long v) { return v >= 0 && v < 0x7fffffffL; }
 template <int AM, int BMD, bool PAIRED, class Epi>
 int run_fast(GemmParams p, LaunchCfg cfg, hipStream_t stream) {
   const void* kern = reinterpret_cast<const void*>(&gemm_fast_kernel<AM, BMD, PAIRED, Epi>);
-  if (int rc = ensure_lds(kern, kFLdsBytes)) return rc;
+  if (int rc = ensure_lds(kern, kFLdsAlloc)) return rc;
   const int cols = PAIRED ? p.H : p.N;
   const int bn_cols = PAIRED ? kFBN / 2 : kFBN;
   p.tiles_m = cdiv(p.M, kFBM);
@@ -128,7 +128,7 @@ int run_fast(GemmParams p, LaunchCfg cfg, hipStream_t stream) {
   const int resident = device_cus();
   dim3 grid(cfg.persistent ? (p.total_tiles < resident ? p.total_tiles : resident) : p.total_tiles,
             splits);
-  hipLaunchKernelGGL((gemm_fast_kernel<AM, BMD, PAIRED, Epi>), grid, dim3(kFNT), kFLdsBytes, stream, p);
+  hipLaunchKernelGGL((gemm_fast_kernel<AM, BMD, PAIRED, Epi>), grid, dim3(kFNT), kFLdsAlloc, stream, p);
   return hip_check(hipGetLastError(), "gemm launch");
 }
 
@@ -136,7 +136,7 @@ int run_fast(GemmParams p, LaunchCfg cfg, hipStream_t stream) {
 // modes already guarantee 16-byte aligned chunks and whole-chunk edges; the per-tile
 // 32-bit offsets are bounded here (paired B tiles reach `half` rows further).
 inline bool fast_ok(const GemmParams& p, int am, int bm, bool paired) {
-  if (am == kGeneric || bm == kGeneric) return false;
+  if (am == kGeneric || bm == kGeneric || !p.vec_out) return false;
   const long lim = 0x7fffffffL;
   const long half = paired ? p.H : 0;
   if (am == kKContig && (256L + 1) * p.a.s_row * 2 >= lim) return false;

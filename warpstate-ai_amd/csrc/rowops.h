@@ -330,3 +330,56 @@ static __global__ void __launch_bounds__(256) splitk_bf16_kernel(const float* __
 }
 
 }  // namespace ws
+
+namespace ws {
+
+// BF16 transpose out[c, r] = in[r, c] of a [rows, cols] matrix with row stride ld_in into a
+// contiguous [cols, rows] result. 64 x 64 tiles through LDS (rows padded by 8 elements so
+// the column reads do not collide); 16-byte global loads and stores when rows, cols and
+// ld_in are multiples of 8 and both pointers are 16-byte aligned. HBM-bound.
+static __global__ void __launch_bounds__(256) transpose_bf16_kernel(
+    const unsigned short* __restrict__ in, long ld_in, unsigned short* __restrict__ out,
+    int rows, int cols, int vec) {
+  __shared__ unsigned short tile[64][72];
+  const int r0 = blockIdx.y * 64, c0 = blockIdx.x * 64;
+  const int t = threadIdx.x;
+  if (vec) {
+    // 64 rows x 8 chunks of 8 columns: two chunks per thread.
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int idx = t + 256 * q, r = idx >> 3, ch = idx & 7;
+      u32x4_t v = {0u, 0u, 0u, 0u};
+      if (r0 + r < rows && c0 + 8 * ch < cols)
+        v = *reinterpret_cast<const u32x4_t*>(in + (long)(r0 + r) * ld_in + c0 + 8 * ch);
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        tile[r][8 * ch + 2 * d] = (unsigned short)(v[d] & 0xffffu);
+        tile[r][8 * ch + 2 * d + 1] = (unsigned short)(v[d] >> 16);
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int idx = t + 256 * q, c = idx >> 3, ch = idx & 7;
+      if (c0 + c < cols && r0 + 8 * ch < rows) {
+        u32x4_t v;
+#pragma unroll
+        for (int d = 0; d < 4; ++d)
+          v[d] = (unsigned)tile[8 * ch + 2 * d][c] | ((unsigned)tile[8 * ch + 2 * d + 1][c] << 16);
+        *reinterpret_cast<u32x4_t*>(out + (long)(c0 + c) * rows + r0 + 8 * ch) = v;
+      }
+    }
+  } else {
+    for (int idx = t; idx < 64 * 64; idx += 256) {
+      const int r = idx >> 6, c = idx & 63;
+      tile[r][c] = (r0 + r < rows && c0 + c < cols) ? in[(long)(r0 + r) * ld_in + c0 + c] : 0;
+    }
+    __syncthreads();
+    for (int idx = t; idx < 64 * 64; idx += 256) {
+      const int c = idx >> 6, r = idx & 63;
+      if (c0 + c < cols && r0 + r < rows) out[(long)(c0 + c) * rows + r0 + r] = tile[r][c];
+    }
+  }
+}
+
+}  // namespace ws

@@ -67,3 +67,16 @@ extern "C" int ws_rmsnorm_backward(const void* x, const float* weight, const flo
                      dweight, groups, (int)d, eager_rounding ? 1 : 0);
   return hip_check(hipGetLastError(), "rmsnorm weight reduce launch");
 }
+
+extern "C" int ws_transpose_bf16(const void* in, int64_t ld_in, void* out, int64_t rows,
+                                 int64_t cols, void* stream) {
+  if (!in || !out) return set_error(kInvalid, "null pointer");
+  if (rows < 1 || cols < 1 || !fits_i32(rows) || !fits_i32(cols) || ld_in < cols)
+    return set_error(kInvalid, "invalid transpose shape");
+  const unsigned long pi = reinterpret_cast<unsigned long>(in), po = reinterpret_cast<unsigned long>(out);
+  const int vec = rows % 8 == 0 && cols % 8 == 0 && ld_in % 8 == 0 && pi % 16 == 0 && po % 16 == 0;
+  hipLaunchKernelGGL(transpose_bf16_kernel, dim3(cdiv(cols, 64), cdiv(rows, 64)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const unsigned short*>(in),
+                     (long)ld_in, static_cast<unsigned short*>(out), (int)rows, (int)cols, vec);
+  return hip_check(hipGetLastError(), "transpose launch");
+}

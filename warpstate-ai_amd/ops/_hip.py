@@ -36,6 +36,7 @@ SIGNATURES = {
     "ws_rmsnorm_backward_partial_floats": (_i64, [_i64, _i64]),
     "ws_rmsnorm_backward": (_i32, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                                    _c_void_p, _c_void_p, _i64, _i64, _i32, _c_void_p]),
+    "ws_transpose_bf16": (_i32, [_c_void_p, _i64, _c_void_p, _i64, _i64, _c_void_p]),
     "ws_rms_rstd": (_i32, [_c_void_p, _i64, _c_void_p, _i64, _i64, _f32, _c_void_p]),
     "ws_rmsnorm_gate_mm": (_i32, [_c_void_p, _i64, _c_void_p, _f32, _c_void_p, _c_void_p,
                                   _c_void_p, _i64, _i64, _c_void_p, _i64, _i64, _i64, _i64,
@@ -53,8 +54,8 @@ SIGNATURES = {
                                     _c_void_p, _c_void_p, _c_void_p]),
     "ws_linear_ce_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64]),
     "ws_linear_ce_backward": (_i32, [_c_void_p, _i64, _c_void_p, _i64, _c_void_p, _c_void_p,
-                                     _c_void_p, _c_void_p, _i64, _i64, _i64, _c_void_p, _i64,
-                                     _c_void_p, _i64, _c_void_p]),
+                                     _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64,
+                                     _c_void_p, _i64, _c_void_p, _i64, _c_void_p]),
 }
 
 _lock = threading.Lock()

@@ -35,9 +35,39 @@ def _check_bf16_cuda(*tensors):
             raise ValueError("Fused matrix kernels require BF16 operands")
 
 
+# Rows of A from which a transposed copy of an N-contiguous B pays for itself: the copy
+# moves 4 |B| bytes once, the GEMM reads B's tiles once per 256-row block of A.
+TRANSPOSE_MIN_ROWS = 1024
+
+
+def transpose(x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Contiguous ``x.T`` of a 2-D BF16 CUDA tensor with unit column stride (HIP kernel)."""
+    _check_bf16_cuda(x)
+    if x.ndim != 2 or x.stride(1) != 1:
+        raise ValueError("transpose expects a 2-D tensor with unit column stride")
+    rows, cols = x.shape
+    if out is None:
+        out = torch.empty((cols, rows), dtype=x.dtype, device=x.device)
+    _hip.call("ws_transpose_bf16", x.data_ptr(), x.stride(0), out.data_ptr(), rows, cols,
+              _hip.stream(x))
+    return out
+
+
+def k_contiguous_b(b: torch.Tensor, rows_a: int) -> torch.Tensor:
+    """B [K, N] as a view whose reduction dim is contiguous: when B is N-contiguous (a
+    weight in an input-gradient GEMM, dX = dY @ W) and A has enough rows to amortize it,
+    a transposed copy W^T [N, K] viewed as [K, N]; otherwise B itself."""
+    if (rows_a >= TRANSPOSE_MIN_ROWS and b.stride(1) == 1 and b.stride(0) >= b.shape[1]
+            and b.shape[0] > 1):
+        return transpose(b).T
+    return b
+
+
 def mm(a: torch.Tensor, b: torch.Tensor, algorithm: str = "tiled", tile: int = 0) -> torch.Tensor:
     """r(a @ b) with the HIP GEMM; `tile` 0 = 256x256, 1 = 128x128."""
     _check_bf16_cuda(a, b)
+    if tile == 0:
+        b = k_contiguous_b(b, a.shape[0])
     m, k = a.shape
     n = b.shape[1]
     out = torch.empty((m, n), dtype=torch.bfloat16, device=a.device)
@@ -113,6 +143,7 @@ def swiglu_backward_mm(grad: torch.Tensor, down_weight: torch.Tensor, packed: to
         raise ValueError("Expected dY [M, d], down weight [d, H], contiguous packed [M, 2H]")
     if out is None:
         out = torch.empty((m, 2 * h), dtype=torch.bfloat16, device=grad.device)
+    down_weight = k_contiguous_b(down_weight, m)
     _hip.call("ws_swiglu_backward_mm", grad.data_ptr(), grad.stride(0), grad.stride(1),
               down_weight.data_ptr(), down_weight.stride(0), down_weight.stride(1),
               packed.data_ptr(), out.data_ptr(), m, h, k, int(eager_rounding), _hip.stream(grad))
@@ -229,8 +260,11 @@ def linear_cross_entropy_backward(hidden: torch.Tensor, weight: torch.Tensor,
     if out is None:
         out = torch.empty((rows, d), dtype=torch.bfloat16, device=hidden.device)
     workspace = state.backward_workspace(d)
+    # The dHidden GEMM reads the head weight along the vocabulary: give it W^T rows.
+    weight_t = transpose(weight) if rows >= TRANSPOSE_MIN_ROWS else None
     _hip.call("ws_linear_ce_backward", hidden.data_ptr(), hidden.stride(0), weight.data_ptr(),
-              weight.stride(0), targets.data_ptr(), state.lse.data_ptr(), state.count.data_ptr(),
+              weight.stride(0), None if weight_t is None else weight_t.data_ptr(),
+              targets.data_ptr(), state.lse.data_ptr(), state.count.data_ptr(),
               grad_mean.data_ptr(), rows, vocab, d, workspace.data_ptr(), state.chunk_rows,
               out.data_ptr(), out.stride(0), _hip.stream(hidden))
     return out

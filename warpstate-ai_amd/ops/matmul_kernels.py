@@ -80,8 +80,15 @@ def policy_key(a, b):
 
 
 def _launch(a, b, algorithm, tile):
-    """Run the HIP GEMM on the current stream into a new row-contiguous BF16 output."""
+    """Run the HIP GEMM on the current stream into a new row-contiguous BF16 output.
+
+    An N-contiguous B (the weight of an input-gradient GEMM) is first copied to a
+    K-contiguous layout when A's rows amortize the copy; the product is unchanged."""
+    from ops.fused_execution import k_contiguous_b
+
     block_m, block_n = tile[0], tile[1]
+    if _hip.tile_code(block_m, block_n) == 0:
+        b = k_contiguous_b(b, a.shape[0])
     m, k = a.shape
     n = b.shape[1]
     output = torch.empty((m, n), device=a.device, dtype=torch.bfloat16)
