@@ -159,9 +159,10 @@ extern "C" int ws_mm_accumulate_f32(const void* a, int64_t a_s0, int64_t a_s1, c
                  p, am, bm, LaunchCfg{0, (int)splits}, s)) {
     return rc;
   }
-  long total = m * n;
-  hipLaunchKernelGGL(splitk_accum_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
+  const int vec = (n % 4 == 0) && (ldg % 4 == 0) && al(g, 16) && al(workspace, 16);
+  const long threads = vec ? m * n / 4 : m * n;
+  hipLaunchKernelGGL(splitk_accum_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s,
                      workspace, (int)splits, (long)(m * n), g, (long)ldg, (int)m, (int)n,
-                     round_bf16 ? 1 : 0);
+                     round_bf16 ? 1 : 0, vec);
   return hip_check(hipGetLastError(), "split-K reduce launch");
 }
