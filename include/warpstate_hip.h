@@ -165,15 +165,19 @@ int64_t ws_linear_ce_workspace_bytes(int64_t rows, int64_t vocab, int64_t d, int
  * the whole batch) go to the 256-byte aligned `workspace` and feed that chunk's dHidden
  * GEMM, split over the vocab with FP32 partials when the chunk alone would not fill the
  * GPU. `weight_t` (nullable) is the head weight transposed, [d, vocab] contiguous; when
- * given, the dHidden GEMM reads it instead of `weight`. Restates autograd of
+ * given, the dHidden GEMM reads it instead of `weight`. `dweight` (nullable, FP32
+ * [vocab, d], row stride ld_dweight) receives the tied head weight's gradient, accumulated
+ * per chunk as dweight += f32(r(G_chunk^T @ hidden_chunk)): the BF16 weight gradient of the
+ * chunk's F.linear followed by FP32 accumulation (warpstate/model.py:321-331 under BF16
+ * autocast, test_gradient_execution.py:243-246). Restates autograd of
  * warpstate/model.py:321-334.
  */
 int ws_linear_ce_backward(const void* hidden, int64_t ld_hidden, const void* weight,
                           int64_t ld_weight, const void* weight_t, const int64_t* targets,
-                          const float* lse,
-                          const float* count, const float* grad_mean, int64_t rows,
-                          int64_t vocab, int64_t d, void* workspace, int64_t chunk_rows,
-                          void* dhidden, int64_t ld_dhidden, void* stream);
+                          const float* lse, const float* count, const float* grad_mean,
+                          int64_t rows, int64_t vocab, int64_t d, void* workspace,
+                          int64_t chunk_rows, void* dhidden, int64_t ld_dhidden, float* dweight,
+                          int64_t ld_dweight, void* stream);
 
 #ifdef __cplusplus
 }

@@ -165,3 +165,28 @@ def linear_cross_entropy_loss_only(hidden, weight, targets, chunk: int = 1024):
                                           ignore_index=-100, reduction="none"))
     loss = torch.cat(losses)
     return loss, loss.sum() / targets.ne(-100).sum().clamp_min(1)
+
+
+def linear_cross_entropy_weight_grad(hidden, weight, targets, chunk: int = 1024,
+                                     grad_mean: float = 1.0):
+    """FP32 gradient of the mean tied-head loss with respect to the head weight
+    [vocab, d], accumulated chunk by chunk as the reference's autocast path does it
+    (warpstate/model.py:321-331; BF16 weight gradient per F.linear call, then FP32
+    AccumulateGrad as in test_gradient_execution.py:243-246):
+    dW += f32(r(G_c^T @ h_c)) with G_c = r(grad_mean (softmax - onehot) / count), zero rows
+    for ignored targets.
+    """
+    count = max(int(targets.ne(-100).sum()), 1)
+    dweight = torch.zeros(weight.shape, dtype=F32)
+    with torch.no_grad():
+        for start in range(0, hidden.shape[0], chunk):
+            h = hidden[start:start + chunk]
+            y = targets[start:start + chunk]
+            logits = F.linear(h, weight).float()
+            soft = torch.softmax(logits, dim=-1)
+            valid = y.ne(-100)
+            onehot = torch.zeros_like(soft)
+            onehot[valid.nonzero().squeeze(1), y[valid]] = 1.0
+            g = ((soft - onehot) * (grad_mean / count)) * valid.unsqueeze(1)
+            dweight += torch.mm(g.to(BF16).T, h).float()
+    return dweight

@@ -276,3 +276,26 @@ def test_standalone_rmsnorm_forward_backward(shape):
     assert_bf16_close(x.grad, x_ref.grad, "rmsnorm dx")
     assert w.grad.dtype == torch.float32
     assert rel_l2(w.grad, w_ref.grad) <= 3e-3
+
+
+@pytest.mark.parametrize("rows,d,vocab,chunk", [(512, 256, 1024, 4096), (3000, 384, 2048, 1024)])
+def test_linear_cross_entropy_head_weight_gradient(rows, d, vocab, chunk):
+    """The tied head weight's FP32 gradient accumulated chunk by chunk, against the
+    oracle with the same chunking; dHidden is unchanged by asking for it."""
+    from ops.benchmark_configs import lm_head_inputs
+    from ops.fused_execution import (CrossEntropyState, linear_cross_entropy_backward,
+                                     linear_cross_entropy_forward)
+
+    inp = lm_head_inputs(m=rows, d=d, vocab=vocab, seed=4)
+    hidden, weight, targets = (inp[k].cuda() for k in ("hidden", "weight", "targets"))
+    state = CrossEntropyState(rows, vocab, hidden.device, chunk_rows=chunk)
+    linear_cross_entropy_forward(hidden, weight, targets, state)
+    one = torch.ones((), device="cuda")
+    dh_plain = linear_cross_entropy_backward(hidden, weight, targets, state, one)
+    wgrad = torch.zeros(vocab, d, device="cuda")
+    dh = linear_cross_entropy_backward(hidden, weight, targets, state, one, weight_grad=wgrad)
+    torch.cuda.synchronize()
+    assert torch.equal(dh, dh_plain)
+    want = oracle.linear_cross_entropy_weight_grad(inp["hidden"], inp["weight"], inp["targets"],
+                                                   chunk=min(chunk, rows))
+    assert_f32_close(wgrad.cpu(), want, "head weight gradient")

@@ -289,3 +289,24 @@ def test_fixture_reference_itself_is_consistent_with_brute_force_small_vocab():
         want = 0.0 if t[i] == -100 else math.log(sum(math.exp(v) for v in logits)) - logits[t[i]]
         assert math.isclose(loss[i], want, rel_tol=1e-12, abs_tol=1e-12)
     assert count == 4
+
+
+def test_head_weight_grad_matches_float64_autograd_and_special_cases():
+    gen = torch.Generator().manual_seed(31)
+    hidden = torch.randn(70, 24, generator=gen).bfloat16()
+    weight = (torch.randn(96, 24, generator=gen) * 0.2).bfloat16()
+    targets = torch.randint(0, 96, (70,), generator=gen)
+    targets[::9] = -100
+    got = oracle.linear_cross_entropy_weight_grad(hidden, weight, targets, chunk=32)
+    w64 = weight.double().requires_grad_(True)
+    logits = hidden.double() @ w64.T
+    loss = F.cross_entropy(logits, targets, ignore_index=-100, reduction="sum") / targets.ne(-100).sum()
+    loss.backward()
+    rel = (got.double() - w64.grad).norm() / w64.grad.norm()
+    assert rel < 2e-2, rel
+    # Ignored rows contribute nothing; all ignored gives an exactly zero gradient.
+    assert torch.count_nonzero(oracle.linear_cross_entropy_weight_grad(
+        hidden, weight, torch.full_like(targets, -100))) == 0
+    # Chunking only changes where the BF16 rounding happens.
+    other = oracle.linear_cross_entropy_weight_grad(hidden, weight, targets, chunk=1024)
+    assert (other - got).norm() / got.norm() < 5e-3

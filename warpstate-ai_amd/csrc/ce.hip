@@ -91,11 +91,12 @@ extern "C" int ws_linear_ce_backward(const void* hidden, int64_t ld_hidden, cons
                                      const float* count, const float* grad_mean, int64_t rows,
                                      int64_t vocab, int64_t d, void* workspace,
                                      int64_t chunk_rows, void* dhidden, int64_t ld_dhidden,
-                                     void* stream) {
+                                     float* dweight, int64_t ld_dweight, void* stream) {
   if (int rc = check_ce(hidden, ld_hidden, weight, ld_weight, targets, rows, vocab, d)) return rc;
   if (!lse || !count || !grad_mean || !workspace || !dhidden) return set_error(kInvalid, "null pointer");
   if (chunk_rows < 1 || !fits_i32(chunk_rows * vocab)) return set_error(kInvalid, "bad chunk_rows");
   if (ld_dhidden < d) return set_error(kInvalid, "dhidden leading dimension < d");
+  if (dweight && ld_dweight < d) return set_error(kInvalid, "dweight leading dimension < d");
   if (reinterpret_cast<unsigned long>(workspace) % 256) return set_error(kInvalid, "workspace must be 256-byte aligned");
   hipStream_t s = static_cast<hipStream_t>(stream);
   const long chunk = chunk_rows < rows ? chunk_rows : rows;
@@ -125,6 +126,24 @@ extern "C" int ws_linear_ce_backward(const void* hidden, int64_t ld_hidden, cons
     } else if (int rc = dispatch<kMaskKK | kMaskGG, WS_TILE_ARGS_LARGE, false, false, EpiCEGrad>(
                    p, am, bm, LaunchCfg{0, 1}, s)) {
       return rc;
+    }
+    // Head weight gradient of the chunk: dW [vocab, d] += f32(r(G^T @ hidden_chunk)).
+    if (dweight) {
+      GemmParams w{};
+      w.a = OperandDesc{gl, 1, vocab};  // G^T [vocab, r]: vocab contiguous
+      w.b = OperandDesc{static_cast<const unsigned short*>(hidden) + start * ld_hidden, 1, ld_hidden};
+      w.M = (int)vocab; w.N = (int)d; w.K = (int)r;
+      w.g = dweight;
+      w.ldg = ld_dweight;
+      w.round_acc = 1;
+      w.vec_out = (d % 4 == 0) && (ld_dweight % 4 == 0) && (reinterpret_cast<unsigned long>(dweight) % 16 == 0);
+      const int wa = operand_mode(w.a, vocab, r, 256), wb = operand_mode(w.b, d, r, 256);
+      if (fast_ok(w, wa, wb, false)) {
+        if (int rc = dispatch_fast<false, FEpiAccF32<false>>(w, wa, wb, LaunchCfg{0, 1}, s)) return rc;
+      } else if (int rc = dispatch<kMaskMM, WS_TILE_ARGS_LARGE, false, false, EpiAccF32<false>>(
+                     w, wa, wb, LaunchCfg{0, 1}, s)) {
+        return rc;
+      }
     }
     // dHidden of the chunk: r(G [r, vocab] @ W [vocab, d]), split over the vocab.
     GemmParams q{};

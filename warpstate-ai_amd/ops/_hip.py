@@ -55,7 +55,8 @@ SIGNATURES = {
     "ws_linear_ce_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64]),
     "ws_linear_ce_backward": (_i32, [_c_void_p, _i64, _c_void_p, _i64, _c_void_p, _c_void_p,
                                      _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64,
-                                     _c_void_p, _i64, _c_void_p, _i64, _c_void_p]),
+                                     _c_void_p, _i64, _c_void_p, _i64, _c_void_p, _i64,
+                                     _c_void_p]),
 }
 
 _lock = threading.Lock()

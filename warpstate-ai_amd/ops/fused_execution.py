@@ -251,8 +251,13 @@ def linear_cross_entropy_forward(hidden: torch.Tensor, weight: torch.Tensor,
 def linear_cross_entropy_backward(hidden: torch.Tensor, weight: torch.Tensor,
                                   targets: torch.Tensor, state: CrossEntropyState,
                                   grad_mean: torch.Tensor,
-                                  out: torch.Tensor | None = None) -> torch.Tensor:
-    """dHidden [rows, d] BF16 of ``mean`` given its FP32 scalar gradient."""
+                                  out: torch.Tensor | None = None,
+                                  weight_grad: torch.Tensor | None = None) -> torch.Tensor:
+    """dHidden [rows, d] BF16 of ``mean`` given its FP32 scalar gradient.
+
+    ``weight_grad`` (FP32 [vocab, d], unit column stride), when given, accumulates the tied
+    head weight's gradient chunk by chunk: weight_grad += f32(r(G_chunk^T @ hidden_chunk)).
+    """
     _check_ce(hidden, weight, targets)
     rows, d = hidden.shape
     vocab = weight.shape[0]
@@ -262,11 +267,17 @@ def linear_cross_entropy_backward(hidden: torch.Tensor, weight: torch.Tensor,
     workspace = state.backward_workspace(d)
     # The dHidden GEMM reads the head weight along the vocabulary: give it W^T rows.
     weight_t = transpose(weight) if rows >= TRANSPOSE_MIN_ROWS else None
+    if weight_grad is not None and (weight_grad.dtype != torch.float32
+                                    or weight_grad.shape != (vocab, d)
+                                    or weight_grad.stride(1) != 1):
+        raise ValueError("weight_grad must be an FP32 [vocab, d] tensor with unit column stride")
     _hip.call("ws_linear_ce_backward", hidden.data_ptr(), hidden.stride(0), weight.data_ptr(),
               weight.stride(0), None if weight_t is None else weight_t.data_ptr(),
               targets.data_ptr(), state.lse.data_ptr(), state.count.data_ptr(),
               grad_mean.data_ptr(), rows, vocab, d, workspace.data_ptr(), state.chunk_rows,
-              out.data_ptr(), out.stride(0), _hip.stream(hidden))
+              out.data_ptr(), out.stride(0),
+              None if weight_grad is None else weight_grad.data_ptr(),
+              0 if weight_grad is None else weight_grad.stride(0), _hip.stream(hidden))
     return out
 
 
