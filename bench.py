@@ -10,8 +10,9 @@ HBM:
   down_fwd     down projection [16384,5632] x [5632,2048] with residual add  (config 3)
   mlp_bwd      SwiGLU MLP backward: dH with fused SwiGLU backward, dX, and FP32-
                accumulated wgrad of W_down and W_upgate                      (config 4)
-  qkv_bwd      input-projection dX [16384,9216] x [9216,2048] and FP32-accumulated
-               wgrad [9216,16384] x [16384,2048]
+  qkv_bwd      backward of qkv_fwd: gradient through the gate sigmoid, dX of the
+               projection [16384,9216] x [9216,2048], FP32-accumulated wgrad
+               [9216,16384] x [16384,2048], RMSNorm backward
 
 ``value`` is the step's algorithmic FLOPs over its wall time (TFLOP/s). The other two
 configurations are timed beside it and reported under ``per_config``: config 1 (SwiGLU
@@ -123,14 +124,15 @@ def run_step(inp, out, timer=None):
     """One hot-path pass; every kernel launches through the C ABI on the current stream."""
     from contextlib import nullcontext
 
+    from ops.activation_execution import _rms_backward
     from ops.fused_execution import (mm, mm_accumulate_, residual_mm, rmsnorm_gate_mm,
-                                     swiglu_backward_mm)
+                                     sigmoid_backward_cols, swiglu_backward_mm)
     from ops.matmul_epilogue import launch_swiglu_mm
 
     reg = timer.region if timer else (lambda name: nullcontext())
     with reg("qkv_fwd"):
         rmsnorm_gate_mm(inp["qkv_x"], inp["qkv_norm_weight"], inp["qkv_eps"], inp["qkv_w"],
-                        GATE, out=out["qkv"], rstd=out["rstd"])
+                        GATE, out=out["qkv"], rstd=out["rstd"], normed=out["qkv_z"])
     with reg("swiglu_fwd"):
         packed, act = launch_swiglu_mm(inp["mlp_x"], inp["mlp_w_upgate"].T, "tiled",
                                        (128, 128, 32, 8, 3), True)
@@ -147,10 +149,13 @@ def run_step(inp, out, timer=None):
         with reg("mlp_bwd.wgrad_upgate"):
             mm_accumulate_(inp["mlp_g_upgate"], dpacked.T, inp["mlp_x"], True)
     with reg("qkv_bwd"):
+        # Backward of RMSNorm -> projection -> gate sigmoid (rmsnorm_gate_mm_backward).
+        dp = sigmoid_backward_cols(inp["qkv_dp"], out["qkv"], GATE, out["qkv_dpg"])
         with reg("qkv_bwd.dx"):
-            mm(inp["qkv_dp"], inp["qkv_w"])
+            dy = mm(dp, inp["qkv_w"])
         with reg("qkv_bwd.wgrad"):
-            mm_accumulate_(inp["qkv_g"], inp["qkv_dp"].T, out["qkv_z"], True)
+            mm_accumulate_(inp["qkv_g"], dp.T, out["qkv_z"], True)
+        _rms_backward(inp["qkv_x"], inp["qkv_norm_weight"], out["rstd"], dy, True)
 
 
 def bench_gpu(args):
@@ -161,11 +166,9 @@ def bench_gpu(args):
            "rstd": torch.empty((m,), dtype=torch.float32, device=device),
            "down": torch.empty((m, D), dtype=torch.bfloat16, device=device),
            "dpacked": torch.empty((m, 2 * FFN), dtype=torch.bfloat16, device=device),
-           # The normalized input saved for the wgrad of the input projection.
-           "qkv_z": torch.empty((m, D), dtype=torch.bfloat16, device=device)}
-    from ops.activation_execution import bf16_rmsnorm
-
-    out["qkv_z"].copy_(bf16_rmsnorm(inp["qkv_x"], inp["qkv_norm_weight"], inp["qkv_eps"])[0])
+           # The normalized input the forward saves for the wgrad of the input projection.
+           "qkv_z": torch.empty((m, D), dtype=torch.bfloat16, device=device),
+           "qkv_dpg": torch.empty((m, NQKV), dtype=torch.bfloat16, device=device)}
     for _ in range(args.warmup):
         run_step(inp, out)
     torch.cuda.synchronize()
@@ -277,7 +280,6 @@ def cpu_baseline(rows):
     gen = torch.Generator("cpu").manual_seed(1)
     dp = (torch.randn((rows, NQKV), generator=gen) * 1e-2).bfloat16()
     g_qkv = torch.randn((NQKV, D), generator=gen) * 1e-4
-    z = oracle.rmsnorm(qkv["x"], qkv["norm_weight"], qkv["eps"])
 
     def step():
         oracle.rmsnorm_gate_projection(qkv["x"], qkv["norm_weight"], qkv["eps"], qkv["w"], GATE)
@@ -285,8 +287,8 @@ def cpu_baseline(rows):
         oracle.residual_projection(down["h"], down["w_down"], down["residual"])
         oracle.mlp_backward(mlp["x"], mlp["w_upgate"], mlp["w_down"], packed, act, mlp["dy"],
                             mlp["g_upgate"], mlp["g_down"])
-        torch.mm(dp, qkv["w"])
-        oracle.accumulate_weight_grad(g_qkv, dp.T, z)
+        oracle.rmsnorm_gate_projection_backward(qkv["x"], qkv["norm_weight"], qkv["eps"],
+                                                qkv["w"], GATE, dp, g_qkv)
 
     step()  # warmup
     times = []

@@ -106,6 +106,14 @@ int ws_rmsnorm_gate_mm(const void* x, int64_t x_s0, const float* norm_weight, fl
                        void* out, int64_t m, int64_t n, int64_t k, int64_t gate_begin,
                        int64_t gate_end, void* stream);
 
+/* Gradient through the gate sigmoid of ws_rmsnorm_gate_mm's output: dp = dout, except
+ * columns [gate_begin, gate_end) where dp = r(dout * (1 - out) * out) with `out` the forward
+ * output (torch.sigmoid's backward, warpstate/model.py:174). dp may be dout itself (then
+ * only the gate columns are rewritten). */
+int ws_sigmoid_backward_cols(const void* dout, int64_t ld_dout, const void* out, int64_t ld_out,
+                             void* dp, int64_t ld_dp, int64_t rows, int64_t cols,
+                             int64_t gate_begin, int64_t gate_end, void* stream);
+
 /* Down projection with residual add: out[m,n] = r(residual[m,n] + r(A @ B)), residual
  * row stride ld_residual (warpstate/model.py:178 under BF16 residuals,
  * ops/residual_experiment.py:25-58). */

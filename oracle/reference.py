@@ -190,3 +190,22 @@ def linear_cross_entropy_weight_grad(hidden, weight, targets, chunk: int = 1024,
             g = ((soft - onehot) * (grad_mean / count)) * valid.unsqueeze(1)
             dweight += torch.mm(g.to(BF16).T, h).float()
     return dweight
+
+
+def rmsnorm_gate_projection_backward(x, norm_weight, eps, weight, gate, dout, weight_grad):
+    """Backward of RMSNorm -> in_proj -> gate sigmoid (warpstate/model.py:22-28, :109,
+    :174) as CPU autograd composes it on BF16 tensors, with the projection weight's BF16
+    gradient accumulated into FP32 (test_gradient_execution.py:243-246).
+    Returns (dx BF16, d norm_weight FP32, weight_grad').
+    """
+    xl = x.detach().clone().requires_grad_(True)
+    wl = norm_weight.detach().clone().requires_grad_(True)
+    y = rmsnorm(xl, wl, eps)
+    yl = y.detach().requires_grad_(True)
+    wt = weight.detach().clone().requires_grad_(True)
+    p = torch.mm(yl, wt.T)
+    begin, end = gate
+    out = torch.cat([p[:, :begin], torch.sigmoid(p[:, begin:end]), p[:, end:]], dim=1)
+    out.backward(dout)
+    y.backward(yl.grad)
+    return xl.grad, wl.grad, weight_grad + wt.grad.float()

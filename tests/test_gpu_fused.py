@@ -299,3 +299,29 @@ def test_linear_cross_entropy_head_weight_gradient(rows, d, vocab, chunk):
     want = oracle.linear_cross_entropy_weight_grad(inp["hidden"], inp["weight"], inp["targets"],
                                                    chunk=min(chunk, rows))
     assert_f32_close(wgrad.cpu(), want, "head weight gradient")
+
+
+@pytest.mark.parametrize("in_place", [False, True])
+@pytest.mark.parametrize("m,d,n,gate", [(512, 256, 576, (384, 512)), (1024, 2048, 9216, (6144, 8192))])
+def test_rmsnorm_gate_projection_backward(m, d, n, gate, in_place):
+    """QKV backward: gate sigmoid backward, dY through W, FP32 wgrad, RMSNorm backward."""
+    from ops.benchmark_configs import rms_projection_inputs
+    from ops.fused_execution import rmsnorm_gate_mm, rmsnorm_gate_mm_backward
+
+    inp = rms_projection_inputs(m=m, d=d, n=n, gate=gate, seed=2)
+    gen = _gen(12)
+    dout = (torch.randn(m, n, generator=gen) * 1e-2).bfloat16()
+    g0 = torch.randn(n, d, generator=gen) * 1e-4
+    x, nw, w = inp["x"].cuda(), inp["norm_weight"].cuda(), inp["w"].cuda()
+    normed = torch.empty_like(x)
+    out, rstd = rmsnorm_gate_mm(x, nw, inp["eps"], w, gate, normed=normed)
+    g = g0.cuda()
+    dx, dnw = rmsnorm_gate_mm_backward(x, nw, rstd, normed, w, gate, out, dout.cuda(), g,
+                                       in_place=in_place)
+    torch.cuda.synchronize()
+    assert_bf16_close(normed, oracle.rmsnorm(inp["x"], inp["norm_weight"], inp["eps"]), "normed")
+    want_dx, want_dnw, want_g = oracle.rmsnorm_gate_projection_backward(
+        inp["x"], inp["norm_weight"], inp["eps"], inp["w"], gate, dout, g0)
+    assert_bf16_close(dx, want_dx, "dx")
+    assert rel_l2(dnw, want_dnw) <= 3e-3
+    assert_f32_close(g.cpu(), want_g, "W_in gradient")

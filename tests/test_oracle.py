@@ -310,3 +310,30 @@ def test_head_weight_grad_matches_float64_autograd_and_special_cases():
     # Chunking only changes where the BF16 rounding happens.
     other = oracle.linear_cross_entropy_weight_grad(hidden, weight, targets, chunk=1024)
     assert (other - got).norm() / got.norm() < 5e-3
+
+
+def test_rmsnorm_gate_backward_matches_float64_autograd():
+    gen = torch.Generator().manual_seed(41)
+    x = torch.randn(40, 64, generator=gen).bfloat16()
+    nw = torch.randn(64, generator=gen) * 0.1 + 1
+    w = (torch.randn(48, 64, generator=gen) * 0.1).bfloat16()
+    dout = torch.randn(40, 48, generator=gen).bfloat16()
+    gate = (16, 32)
+    dx, dnw, g = oracle.rmsnorm_gate_projection_backward(x, nw, 1e-6, w, gate, dout,
+                                                         torch.zeros(48, 64))
+    x64 = x.double().requires_grad_(True)
+    nw64 = nw.double().requires_grad_(True)
+    w64 = w.double().requires_grad_(True)
+    y = x64 * torch.rsqrt(x64.pow(2).mean(-1, keepdim=True) + 1e-6) * nw64
+    p = y @ w64.T
+    out = torch.cat([p[:, :16], torch.sigmoid(p[:, 16:32]), p[:, 32:]], dim=1)
+    out.backward(dout.double())
+    for got, want in ((dx, x64.grad), (dnw, nw64.grad), (g, w64.grad)):
+        assert ((got.double() - want).norm() / want.norm()) < 2e-2
+    # The gate columns' gradient vanishes with the sigmoid's derivative: a zero dout on the
+    # other columns leaves the weight gradient zero on those rows.
+    d2 = dout.clone()
+    d2[:, :16] = 0
+    d2[:, 32:] = 0
+    _, _, g2 = oracle.rmsnorm_gate_projection_backward(x, nw, 1e-6, w, gate, d2, torch.zeros(48, 64))
+    assert torch.count_nonzero(g2[:16]) == 0 and torch.count_nonzero(g2[32:]) == 0

@@ -125,69 +125,110 @@ static __global__ void __launch_bounds__(256) rmsnorm_fwd_kernel(const unsigned 
 }
 
 // RMSNorm backward (ops/activation_execution.py:113-141): per row
-//   z = x r, dz = dy w (both BF16-rounded when eager), dr = sum(dz x),
-//   dx = dz r + (-0.5 dr r^3 / D) * 2x; per-group partial weight gradient sum(dy z).
-// One wave per row, `rows_per_block` rows per block write one partial row each.
+//   z = r?(x r), dz = r?(dy r?(w)), dr = sum(dz x), dx = dz r + (-0.5 dr r^3 / D) * 2x,
+// and the weight-gradient partial sum over this block's rows of r?(dy z) (r? = BF16
+// rounding when eager). One wave per row, 16-byte loads: lane l owns columns
+// 8 l + 512 s (s < SEGS), and keeps its x and dy chunks in registers between the two
+// passes over the row. A block of 4 waves takes kRmsRowsPerBlock consecutive rows and writes
+// one partial weight-gradient row (summed across its waves in LDS).
+constexpr int kRmsRowsPerBlock = 64;
+
+template <int SEGS>
 static __global__ void __launch_bounds__(256) rmsnorm_bwd_kernel(
     const unsigned short* __restrict__ x, const float* __restrict__ w,
     const float* __restrict__ rstd, const unsigned short* __restrict__ dy,
     unsigned short* __restrict__ dx, float* __restrict__ dw_part, int rows, int D, int eager) {
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int row = blockIdx.x * 4 + wave;
-  const bool live = row < rows;
-  const float r = live ? rstd[row] : 0.0f;
-  float dr = 0.0f;
-  if (live) {
-    for (int c = lane; c < D; c += 64) {
-      float xv = bf16_bits_to_f32(x[(long)row * D + c]);
-      float wc = w[c];
-      if (eager) wc = rbf16(wc);
-      float dz = bf16_bits_to_f32(dy[(long)row * D + c]) * wc;
-      if (eager) dz = rbf16(dz);
-      dr += dz * xv;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  float wb[SEGS][8];
+#pragma unroll
+  for (int s = 0; s < SEGS; ++s) {
+    const int c = 8 * lane + 512 * s;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float v = c + e < D ? w[c + e] : 0.0f;
+      wb[s][e] = eager ? rbf16(v) : v;
     }
   }
-  dr = wave_sum(dr);
-  const float dsq = (-0.5f * dr * (r * r * r)) / (float)D;
-  if (live) {
-    for (int c = lane; c < D; c += 64) {
-      float xv = bf16_bits_to_f32(x[(long)row * D + c]);
-      float wc = w[c];
-      if (eager) wc = rbf16(wc);
-      float dz = bf16_bits_to_f32(dy[(long)row * D + c]) * wc;
-      if (eager) dz = rbf16(dz);
-      dx[(long)row * D + c] = to_bf16_bits(dz * r + dsq * (2.0f * xv));
+  float part[SEGS][8];
+#pragma unroll
+  for (int s = 0; s < SEGS; ++s)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) part[s][e] = 0.0f;
+
+  const int row_end = min(rows, (blockIdx.x + 1) * kRmsRowsPerBlock);
+  for (int row = blockIdx.x * kRmsRowsPerBlock + wave; row < row_end; row += 4) {
+    const float r = rstd[row];
+    u32x4_t xv[SEGS], gv[SEGS];
+    float dr = 0.0f;
+#pragma unroll
+    for (int s = 0; s < SEGS; ++s) {
+      const int c = 8 * lane + 512 * s;
+      const bool ok = c < D;
+      xv[s] = ok ? *reinterpret_cast<const u32x4_t*>(x + (long)row * D + c) : u32x4_t{0u, 0u, 0u, 0u};
+      gv[s] = ok ? *reinterpret_cast<const u32x4_t*>(dy + (long)row * D + c) : u32x4_t{0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        float dz0 = lo_bf16(gv[s][d]) * wb[s][2 * d], dz1 = hi_bf16(gv[s][d]) * wb[s][2 * d + 1];
+        if (eager) { dz0 = rbf16(dz0); dz1 = rbf16(dz1); }
+        dr += dz0 * lo_bf16(xv[s][d]);
+        dr += dz1 * hi_bf16(xv[s][d]);
+      }
+    }
+    dr = wave_sum(dr);
+    const float dsq = (-0.5f * dr * (r * r * r)) / (float)D;
+#pragma unroll
+    for (int s = 0; s < SEGS; ++s) {
+      const int c = 8 * lane + 512 * s;
+      u32x4_t o;
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        float v2[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const float xs = h ? hi_bf16(xv[s][d]) : lo_bf16(xv[s][d]);
+          const float gs = h ? hi_bf16(gv[s][d]) : lo_bf16(gv[s][d]);
+          float dz = gs * wb[s][2 * d + h];
+          if (eager) dz = rbf16(dz);
+          v2[h] = dz * r + dsq * (2.0f * xs);
+          float z = xs * r;
+          if (eager) z = rbf16(z);
+          float pv = gs * z;
+          if (eager) pv = rbf16(pv);
+          part[s][2 * d + h] += pv;
+        }
+        o[d] = pack_bf16x2(v2[0], v2[1]);
+      }
+      if (c < D) *reinterpret_cast<u32x4_t*>(dx + (long)row * D + c) = o;
     }
   }
-  // Weight-gradient partial for this block's 4 rows, in row order.
-  extern __shared__ float part[];  // [4][D]
-  for (int c = lane; c < D; c += 64) {
-    float v = 0.0f;
-    if (live) {
-      float z = bf16_bits_to_f32(x[(long)row * D + c]) * r;
-      if (eager) z = rbf16(z);
-      v = bf16_bits_to_f32(dy[(long)row * D + c]) * z;
-      if (eager) v = rbf16(v);
+  // Sum the four waves' partials in LDS, then one row per block.
+  extern __shared__ float lds_part[];  // [4][D]
+#pragma unroll
+  for (int s = 0; s < SEGS; ++s) {
+    const int c = 8 * lane + 512 * s;
+    if (c < D) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) lds_part[wave * D + c + e] = part[s][e];
     }
-    part[wave * D + c] = v;
   }
   __syncthreads();
-  for (int c = threadIdx.x; c < D; c += blockDim.x) {
-    dw_part[(long)blockIdx.x * D + c] = ((part[c] + part[D + c]) + part[2 * D + c]) + part[3 * D + c];
-  }
+  for (int c = threadIdx.x; c < D; c += blockDim.x)
+    dw_part[(long)blockIdx.x * D + c] =
+        ((lds_part[c] + lds_part[D + c]) + lds_part[2 * D + c]) + lds_part[3 * D + c];
 }
 
-// Column sum of the weight-gradient partials (ops/activation_execution.py:144-158).
+// Column sum of the weight-gradient partials (ops/activation_execution.py:144-158): four
+// columns per thread, partial rows summed in order.
 static __global__ void __launch_bounds__(256) rms_weight_reduce_kernel(const float* __restrict__ part,
                                                                 float* __restrict__ dw, int groups,
                                                                 int D, int eager) {
-  const int c = blockIdx.x * blockDim.x + threadIdx.x;
+  const int c = 4 * (blockIdx.x * blockDim.x + threadIdx.x);
   if (c >= D) return;
-  float total = 0.0f;
-  for (int gidx = 0; gidx < groups; ++gidx) total += part[(long)gidx * D + c];
-  if (eager) total = rbf16(total);
-  dw[c] = total;
+  f32x4_t total = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int gidx = 0; gidx < groups; ++gidx)
+    total += *reinterpret_cast<const f32x4_t*>(part + (long)gidx * D + c);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) dw[c + e] = eager ? rbf16(total[e]) : total[e];
 }
 
 // ---------------------------------------------------------------------------------------
@@ -395,6 +436,53 @@ static __global__ void __launch_bounds__(256) transpose_bf16_kernel(
       if (c0 + c < cols && r0 + r < rows) out[(long)(c0 + c) * rows + r0 + r] = tile[r][c];
     }
   }
+}
+
+}  // namespace ws
+
+namespace ws {
+
+// Gradient through the gate sigmoid of the fused input projection: for columns
+// [col_lo, col_hi) of a [rows, *] gradient, dp = r(dout * (1 - s) * s) with s the BF16
+// sigmoid output (torch's sigmoid backward, evaluated in FP32), other columns in
+// [c0, c1) are copied. Processes columns [c0, c1) of every row; 8 columns per thread
+// with 16-byte accesses when `vec`.
+static __global__ void __launch_bounds__(256) sigmoid_backward_cols_kernel(
+    const unsigned short* __restrict__ dout, long ld_dout, const unsigned short* __restrict__ s,
+    long ld_s, unsigned short* dp, long ld_dp, int rows, int c0, int c1, int col_lo, int col_hi,
+    int vec) {
+  const int width = c1 - c0;
+  if (vec) {
+    const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    const int per_row = width / 8;
+    if (idx >= (long)rows * per_row) return;
+    const long r = idx / per_row;
+    const int c = c0 + 8 * (int)(idx % per_row);
+    u32x4_t g = *reinterpret_cast<const u32x4_t*>(dout + r * ld_dout + c);
+    if (c + 8 > col_lo && c < col_hi) {
+      const u32x4_t sv = *reinterpret_cast<const u32x4_t*>(s + r * ld_s + c);
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        float lo = lo_bf16(g[d]), hi = hi_bf16(g[d]);
+        const float slo = lo_bf16(sv[d]), shi = hi_bf16(sv[d]);
+        if (c + 2 * d >= col_lo && c + 2 * d < col_hi) lo = (lo * (1.0f - slo)) * slo;
+        if (c + 2 * d + 1 >= col_lo && c + 2 * d + 1 < col_hi) hi = (hi * (1.0f - shi)) * shi;
+        g[d] = pack_bf16x2(lo, hi);
+      }
+    }
+    *reinterpret_cast<u32x4_t*>(dp + r * ld_dp + c) = g;
+    return;
+  }
+  const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (long)rows * width) return;
+  const long r = idx / width;
+  const int c = c0 + (int)(idx % width);
+  float g = bf16_bits_to_f32(dout[r * ld_dout + c]);
+  if (c >= col_lo && c < col_hi) {
+    const float sv = bf16_bits_to_f32(s[r * ld_s + c]);
+    g = (g * (1.0f - sv)) * sv;
+  }
+  dp[r * ld_dp + c] = to_bf16_bits(g);
 }
 
 }  // namespace ws

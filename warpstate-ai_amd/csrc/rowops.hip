@@ -44,7 +44,20 @@ extern "C" int ws_rmsnorm_forward(const void* x, const float* weight, void* y, f
 }
 
 extern "C" int64_t ws_rmsnorm_backward_partial_floats(int64_t rows, int64_t d) {
-  return (int64_t)cdiv(rows, 4) * d;
+  return (int64_t)cdiv(rows, kRmsRowsPerBlock) * d;
+}
+
+template <int SEGS>
+static int launch_rms_bwd(const void* x, const float* weight, const float* rstd, const void* grad,
+                          void* dx, float* partial, int rows, int d, int eager, hipStream_t s) {
+  const int lds = 4 * d * (int)sizeof(float);
+  const void* kern = reinterpret_cast<const void*>(&rmsnorm_bwd_kernel<SEGS>);
+  if (int rc = ensure_lds(kern, lds)) return rc;
+  hipLaunchKernelGGL(rmsnorm_bwd_kernel<SEGS>, dim3(cdiv(rows, kRmsRowsPerBlock)), dim3(256), lds, s,
+                     static_cast<const unsigned short*>(x), weight, rstd,
+                     static_cast<const unsigned short*>(grad), static_cast<unsigned short*>(dx),
+                     partial, rows, d, eager);
+  return hip_check(hipGetLastError(), "rmsnorm backward launch");
 }
 
 extern "C" int ws_rmsnorm_backward(const void* x, const float* weight, const float* rstd,
@@ -53,18 +66,24 @@ extern "C" int ws_rmsnorm_backward(const void* x, const float* weight, const flo
   if (!x || !weight || !rstd || !grad || !dx || !dweight || !partial)
     return set_error(kInvalid, "null pointer");
   if (rows < 1 || d < 1 || !fits_i32(rows) || !fits_i32(d)) return set_error(kInvalid, "invalid RMSNorm shape");
-  if (d * 4 * 4 > 160 * 1024) return set_error(kInvalid, "RMSNorm width %ld exceeds the LDS budget", (long)d);
+  if (d > 8192 || d % 8 != 0)
+    return set_error(kInvalid, "RMSNorm backward needs a width that is a multiple of 8, at most 8192 (got %ld)", (long)d);
+  const unsigned long a = reinterpret_cast<unsigned long>(x) | reinterpret_cast<unsigned long>(grad) |
+                          reinterpret_cast<unsigned long>(dx) | reinterpret_cast<unsigned long>(weight) |
+                          reinterpret_cast<unsigned long>(partial);
+  if (a % 16) return set_error(kInvalid, "RMSNorm backward needs 16-byte aligned buffers");
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const int groups = cdiv(rows, 4);
-  const int lds = (int)(4 * d * sizeof(float));
-  if (int rc = ensure_lds(reinterpret_cast<const void*>(&rmsnorm_bwd_kernel), lds)) return rc;
-  hipLaunchKernelGGL(rmsnorm_bwd_kernel, dim3(groups), dim3(256), lds, s,
-                     static_cast<const unsigned short*>(x), weight, rstd,
-                     static_cast<const unsigned short*>(grad), static_cast<unsigned short*>(dx),
-                     partial, (int)rows, (int)d, eager_rounding ? 1 : 0);
-  if (int rc = hip_check(hipGetLastError(), "rmsnorm backward launch")) return rc;
-  hipLaunchKernelGGL(rms_weight_reduce_kernel, dim3(cdiv(d, 256)), dim3(256), 0, s, partial,
-                     dweight, groups, (int)d, eager_rounding ? 1 : 0);
+  const int segs = cdiv(d, 512), e = eager_rounding ? 1 : 0;
+  int rc;
+  if (segs <= 1) rc = launch_rms_bwd<1>(x, weight, rstd, grad, dx, partial, (int)rows, (int)d, e, s);
+  else if (segs <= 2) rc = launch_rms_bwd<2>(x, weight, rstd, grad, dx, partial, (int)rows, (int)d, e, s);
+  else if (segs <= 4) rc = launch_rms_bwd<4>(x, weight, rstd, grad, dx, partial, (int)rows, (int)d, e, s);
+  else if (segs <= 8) rc = launch_rms_bwd<8>(x, weight, rstd, grad, dx, partial, (int)rows, (int)d, e, s);
+  else rc = launch_rms_bwd<16>(x, weight, rstd, grad, dx, partial, (int)rows, (int)d, e, s);
+  if (rc) return rc;
+  const int groups = cdiv(rows, kRmsRowsPerBlock);
+  hipLaunchKernelGGL(rms_weight_reduce_kernel, dim3(cdiv(d / 4, 256)), dim3(256), 0, s, partial,
+                     dweight, groups, (int)d, e);
   return hip_check(hipGetLastError(), "rmsnorm weight reduce launch");
 }
 
@@ -79,4 +98,37 @@ extern "C" int ws_transpose_bf16(const void* in, int64_t ld_in, void* out, int64
                      static_cast<hipStream_t>(stream), static_cast<const unsigned short*>(in),
                      (long)ld_in, static_cast<unsigned short*>(out), (int)rows, (int)cols, vec);
   return hip_check(hipGetLastError(), "transpose launch");
+}
+
+extern "C" int ws_sigmoid_backward_cols(const void* dout, int64_t ld_dout, const void* out,
+                                        int64_t ld_out, void* dp, int64_t ld_dp, int64_t rows,
+                                        int64_t cols, int64_t gate_begin, int64_t gate_end,
+                                        void* stream) {
+  if (!dout || !out || !dp) return set_error(kInvalid, "null pointer");
+  if (rows < 1 || cols < 1 || !fits_i32(rows) || !fits_i32(cols) || ld_dout < cols ||
+      ld_out < cols || ld_dp < cols)
+    return set_error(kInvalid, "invalid gradient shape");
+  if (gate_begin < 0 || gate_end < gate_begin || gate_end > cols)
+    return set_error(kInvalid, "gate column range [%ld, %ld) outside [0, %ld)", (long)gate_begin,
+                     (long)gate_end, (long)cols);
+  // In place only the gate columns change; otherwise every column is written.
+  const bool in_place = dp == dout && ld_dp == ld_dout;
+  long c0 = in_place ? gate_begin : 0, c1 = in_place ? gate_end : cols;
+  if (in_place) {  // widen to whole 8-column groups so the vector path applies
+    c0 = c0 / 8 * 8;
+    c1 = (c1 + 7) / 8 * 8 < cols ? (c1 + 7) / 8 * 8 : cols;
+  }
+  if (c1 <= c0) return kOk;
+  const unsigned long a = reinterpret_cast<unsigned long>(dout) | reinterpret_cast<unsigned long>(out) |
+                          reinterpret_cast<unsigned long>(dp);
+  const int vec = a % 16 == 0 && ld_dout % 8 == 0 && ld_out % 8 == 0 && ld_dp % 8 == 0 &&
+                  c0 % 8 == 0 && (c1 - c0) % 8 == 0;
+  const long threads = vec ? rows * ((c1 - c0) / 8) : rows * (c1 - c0);
+  hipLaunchKernelGGL(sigmoid_backward_cols_kernel, dim3((unsigned)((threads + 255) / 256)),
+                     dim3(256), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const unsigned short*>(dout), (long)ld_dout,
+                     static_cast<const unsigned short*>(out), (long)ld_out,
+                     static_cast<unsigned short*>(dp), (long)ld_dp, (int)rows, (int)c0, (int)c1,
+                     (int)gate_begin, (int)gate_end, vec);
+  return hip_check(hipGetLastError(), "sigmoid backward launch");
 }

@@ -41,6 +41,8 @@ SIGNATURES = {
     "ws_rmsnorm_gate_mm": (_i32, [_c_void_p, _i64, _c_void_p, _f32, _c_void_p, _c_void_p,
                                   _c_void_p, _i64, _i64, _c_void_p, _i64, _i64, _i64, _i64,
                                   _i64, _c_void_p]),
+    "ws_sigmoid_backward_cols": (_i32, [_c_void_p, _i64, _c_void_p, _i64, _c_void_p, _i64, _i64,
+                                        _i64, _i64, _i64, _c_void_p]),
     "ws_residual_mm": (_i32, [_c_void_p, _i64, _i64, _c_void_p, _i64, _i64, _c_void_p, _i64,
                               _c_void_p, _i64, _i64, _i64, _c_void_p]),
     "ws_swiglu_backward_mm": (_i32, [_c_void_p, _i64, _i64, _c_void_p, _i64, _i64, _c_void_p,

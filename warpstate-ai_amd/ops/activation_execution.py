@@ -85,6 +85,7 @@ def _rms_backward(x: torch.Tensor, weight: torch.Tensor, rstd: torch.Tensor,
                   grad: torch.Tensor, eager_rounding: bool) -> tuple[torch.Tensor, torch.Tensor]:
     """dX (BF16) and the FP32 weight gradient (ops/activation_execution.py:176-194)."""
     grad = grad.contiguous()
+    x = x.contiguous()
     width = x.shape[-1]
     rows = x.numel() // width
     output = torch.empty_like(x)

@@ -113,6 +113,43 @@ def rmsnorm_gate_mm(x: torch.Tensor, norm_weight: torch.Tensor, eps: float,
     return out, rstd
 
 
+def sigmoid_backward_cols(dout: torch.Tensor, out: torch.Tensor, gate: tuple[int, int],
+                          dp: torch.Tensor | None = None) -> torch.Tensor:
+    """Gradient of the projection before the gate sigmoid: dout with columns [gate)
+    replaced by r(dout (1 - out) out). ``dp=dout`` rewrites only the gate columns in place."""
+    _check_bf16_cuda(dout, out)
+    if dout.shape != out.shape or dout.stride(1) != 1 or out.stride(1) != 1:
+        raise ValueError("dout and out must be matching [M, N] tensors with unit column stride")
+    if dp is None:
+        dp = torch.empty_like(dout)
+    rows, cols = dout.shape
+    _hip.call("ws_sigmoid_backward_cols", dout.data_ptr(), dout.stride(0), out.data_ptr(),
+              out.stride(0), dp.data_ptr(), dp.stride(0), rows, cols, int(gate[0]),
+              int(gate[1]), _hip.stream(dout))
+    return dp
+
+
+def rmsnorm_gate_mm_backward(x: torch.Tensor, norm_weight: torch.Tensor, rstd: torch.Tensor,
+                             normed: torch.Tensor, weight: torch.Tensor, gate: tuple[int, int],
+                             out: torch.Tensor, dout: torch.Tensor, weight_grad: torch.Tensor,
+                             eager_rounding: bool = True, in_place: bool = False
+                             ) -> tuple[torch.Tensor, torch.Tensor]:
+    """Backward of ``rmsnorm_gate_mm``: returns (dx BF16 [M, K], d norm_weight FP32 [K]) and
+    accumulates the projection weight's gradient, weight_grad [N, K] += f32(r(dP^T y)).
+
+    dP is dout through the gate sigmoid (``sigmoid_backward_cols``; ``in_place`` reuses
+    dout's storage), dy = r(dP @ W) (ops/matmul_execution.py:239), then the RMSNorm
+    backward of ops/activation_execution.py:113-158 with the saved rstd.
+    """
+    from ops.activation_execution import _rms_backward
+
+    dp = sigmoid_backward_cols(dout, out, gate, dout if in_place else None)
+    dy = mm(dp, weight)
+    mm_accumulate_(weight_grad, dp.T, normed, True)
+    dx, dnorm = _rms_backward(x, norm_weight, rstd, dy, eager_rounding)
+    return dx, dnorm
+
+
 def residual_mm(a: torch.Tensor, weight: torch.Tensor, residual: torch.Tensor,
                 out: torch.Tensor | None = None) -> torch.Tensor:
     """r(residual + r(a @ weight.T)); a [M, K], weight [N, K], residual [M, N] (unit
