@@ -149,8 +149,10 @@ def run_step(inp, out, timer=None):
         with reg("mlp_bwd.wgrad_upgate"):
             mm_accumulate_(inp["mlp_g_upgate"], dpacked.T, inp["mlp_x"], True)
     with reg("qkv_bwd"):
-        # Backward of RMSNorm -> projection -> gate sigmoid (rmsnorm_gate_mm_backward).
-        dp = sigmoid_backward_cols(inp["qkv_dp"], out["qkv"], GATE, out["qkv_dpg"])
+        # Backward of RMSNorm -> projection -> gate sigmoid (rmsnorm_gate_mm_backward with
+        # in_place=True): the incoming gradient of the projection output has no other
+        # consumer, so the sigmoid backward rewrites its gate columns in place.
+        dp = sigmoid_backward_cols(inp["qkv_dp"], out["qkv"], GATE, inp["qkv_dp"])
         with reg("qkv_bwd.dx"):
             dy = mm(dp, inp["qkv_w"])
         with reg("qkv_bwd.wgrad"):
@@ -167,8 +169,7 @@ def bench_gpu(args):
            "down": torch.empty((m, D), dtype=torch.bfloat16, device=device),
            "dpacked": torch.empty((m, 2 * FFN), dtype=torch.bfloat16, device=device),
            # The normalized input the forward saves for the wgrad of the input projection.
-           "qkv_z": torch.empty((m, D), dtype=torch.bfloat16, device=device),
-           "qkv_dpg": torch.empty((m, NQKV), dtype=torch.bfloat16, device=device)}
+           "qkv_z": torch.empty((m, D), dtype=torch.bfloat16, device=device)}
     for _ in range(args.warmup):
         run_step(inp, out)
     torch.cuda.synchronize()
@@ -212,6 +213,32 @@ def bench_gpu(args):
     hbm = {"rms_rstd": {"ms": round(rstd_ms, 4), "bytes": rstd_bytes,
                         "gbs": round(rstd_bytes / rstd_ms / 1e6, 1)}}
     return wall_ms, sum(flops.values()), regions, kernels, hbm, inp, out
+
+
+def bench_layout(args, device):
+    """Packed attention-backward gradient layout at the reference's profile shape
+    (4, 16, 32, 128, 64): HBM-bound, 12 BF16 inputs read and 5 BF16 sections written per
+    element. "single" is the product path; "profile" is the two-pass scratch baseline."""
+    from ops.backward_layout import PROFILE_SHAPE, make_inputs, prepare_layout
+
+    inputs = make_inputs(PROFILE_SHAPE, device=device, seed=817)
+    b, n, h, c, d = PROFILE_SHAPE
+    out = torch.empty((b, n * c, 5 * h * d), dtype=torch.bfloat16, device=device)
+    ops = {"single": prepare_layout(inputs, "single", output=out),
+           "profile": prepare_layout(inputs, "profile", output=out)}
+    timer = Timer()
+    for name, operation in ops.items():
+        for _ in range(args.warmup):
+            operation()
+        for _ in range(args.steps):
+            with timer.region(name):
+                operation()
+    torch.cuda.synchronize()
+    nbytes = 34 * inputs.q_memory.numel()
+    ms = timer.mean_ms("single")
+    return {"ms": round(ms, 4), "bytes": nbytes, "gbs": round(nbytes / ms / 1e6, 1),
+            "frac_hbm": round(nbytes / ms / 1e6 / PEAK_HBM_GBS, 4),
+            "profile_baseline_ms": round(timer.mean_ms("profile"), 4)}
 
 
 def bench_extra(args, device):
@@ -317,6 +344,8 @@ def main():
     del inp, out
     torch.cuda.empty_cache()
     per_config = {} if args.no_extra else bench_extra(args, device)
+    if not args.no_extra:
+        hbm["attention_bwd_layout_4x16x32x128x64"] = bench_layout(args, device)
     value = step_flops / wall_ms / 1e9
     dom_name = max(kernels, key=lambda k: kernels[k]["ms"])
     dom = kernels[dom_name]

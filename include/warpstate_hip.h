@@ -187,6 +187,26 @@ int ws_linear_ce_backward(const void* hidden, int64_t ld_hidden, const void* wei
                           int64_t chunk_rows, void* dhidden, int64_t ld_dhidden, float* dweight,
                           int64_t ld_dweight, void* stream);
 
+/*
+ * Packed attention-backward gradient layout: out [B, N*C, 5*H*D] BF16 (token-major rows of
+ * [q | k | v | gate | u], each H*D wide) from the saved head-major [B, N, H, C, D] BF16
+ * tensors q_memory, q_local, tanh_k, k_local, v_local, memory, local, gate, u_write, tanh_u,
+ * k_write [B, N, H, D, C], grad_y [B, N*C, H*D] and FP32 rope tables sin, cos [C, D]; all
+ * contiguous. `scale` multiplies memory in the gate gradient (head_dim^-0.5).
+ * `algorithm`: 0 = "profile" (two passes through the caller's head-major BF16 scratch_q and
+ * scratch_k, the reference's profiled two-kernel baseline), 1 = "paired" (q/k pass, then
+ * v/gate/u pass), 2 = "single" (one pass). All three give identical bits. Replaces the
+ * launches of prepare_layout (ops/backward_layout.py:213-276) of the kernels at :116-210.
+ */
+int ws_backward_layout(const void* q_memory, const void* q_local, const float* sin,
+                       const float* cos, const void* k_write, const void* tanh_k,
+                       const void* k_local, const void* v_local, const void* grad_y,
+                       const void* memory, const void* local, const void* gate,
+                       const void* u_write, const void* tanh_u, void* out, int64_t batch,
+                       int64_t chunks, int64_t heads, int64_t chunk_size, int64_t head_dim,
+                       float scale, int algorithm, void* scratch_q, void* scratch_k,
+                       void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -217,18 +217,34 @@ static __global__ void __launch_bounds__(256) rmsnorm_bwd_kernel(
         ((lds_part[c] + lds_part[D + c]) + lds_part[2 * D + c]) + lds_part[3 * D + c];
 }
 
-// Column sum of the weight-gradient partials (ops/activation_execution.py:144-158): four
-// columns per thread, partial rows summed in order.
+// Column sum of the weight-gradient partials (ops/activation_execution.py:144-158). A
+// block owns 32 columns: thread (lane g, quad q) sums columns 4q..4q+3 over the partial
+// rows g, g + 32, g + 64, ... in order, then the 32 lane sums are added in a fixed
+// pairwise tree, so the result is deterministic. D % 4 == 0.
+constexpr int kRmsReduceCols = 32, kRmsReduceLanes = 32;
 static __global__ void __launch_bounds__(256) rms_weight_reduce_kernel(const float* __restrict__ part,
                                                                 float* __restrict__ dw, int groups,
                                                                 int D, int eager) {
-  const int c = 4 * (blockIdx.x * blockDim.x + threadIdx.x);
-  if (c >= D) return;
+  __shared__ f32x4_t sums[kRmsReduceLanes][kRmsReduceCols / 4];
+  const int q = threadIdx.x & 7, g0 = threadIdx.x >> 3;
+  const int c = blockIdx.x * kRmsReduceCols + 4 * q;
   f32x4_t total = {0.0f, 0.0f, 0.0f, 0.0f};
-  for (int gidx = 0; gidx < groups; ++gidx)
-    total += *reinterpret_cast<const f32x4_t*>(part + (long)gidx * D + c);
+  if (c < D) {
+#pragma unroll 8
+    for (int g = g0; g < groups; g += kRmsReduceLanes)
+      total += *reinterpret_cast<const f32x4_t*>(part + (long)g * D + c);
+  }
+  sums[g0][q] = total;
+  __syncthreads();
 #pragma unroll
-  for (int e = 0; e < 4; ++e) dw[c + e] = eager ? rbf16(total[e]) : total[e];
+  for (int width = kRmsReduceLanes / 2; width >= 1; width >>= 1) {
+    if (g0 < width) sums[g0][q] += sums[g0 + width][q];
+    __syncthreads();
+  }
+  if (g0 == 0 && c < D) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) dw[c + e] = eager ? rbf16(sums[0][q][e]) : sums[0][q][e];
+  }
 }
 
 // ---------------------------------------------------------------------------------------

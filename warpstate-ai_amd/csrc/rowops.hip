@@ -82,7 +82,7 @@ extern "C" int ws_rmsnorm_backward(const void* x, const float* weight, const flo
   else rc = launch_rms_bwd<16>(x, weight, rstd, grad, dx, partial, (int)rows, (int)d, e, s);
   if (rc) return rc;
   const int groups = cdiv(rows, kRmsRowsPerBlock);
-  hipLaunchKernelGGL(rms_weight_reduce_kernel, dim3(cdiv(d / 4, 256)), dim3(256), 0, s, partial,
+  hipLaunchKernelGGL(rms_weight_reduce_kernel, dim3(cdiv(d, kRmsReduceCols)), dim3(256), 0, s, partial,
                      dweight, groups, (int)d, e);
   return hip_check(hipGetLastError(), "rmsnorm weight reduce launch");
 }

@@ -59,6 +59,8 @@ SIGNATURES = {
                                      _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64,
                                      _c_void_p, _i64, _c_void_p, _i64, _c_void_p, _i64,
                                      _c_void_p]),
+    "ws_backward_layout": (_i32, [_c_void_p] * 15 + [_i64] * 5 + [_f32, _i32, _c_void_p,
+                                                                   _c_void_p, _c_void_p]),
 }
 
 _lock = threading.Lock()

@@ -27,6 +27,29 @@ class RMSNorm(nn.Module):
         return wide.to(x.dtype) * self.weight.to(x.dtype)
 
 
+def rotate_half(x: torch.Tensor) -> torch.Tensor:
+    """Interleaved rotary pairing (warpstate/model.py:31-34): lane pair (2i, 2i+1) maps
+    (a, b) to (-b, a)."""
+    pairs = x.unflatten(-1, (-1, 2))
+    return torch.stack((-pairs[..., 1], pairs[..., 0]), dim=-1).flatten(-2)
+
+
+def rope_cos_sin(length: int, dim: int, device: torch.device, dtype: torch.dtype
+                 ) -> tuple[torch.Tensor, torch.Tensor]:
+    """[length, dim] rotary tables with each frequency repeated for its lane pair
+    (warpstate/model.py:37-42): angle(t, 2i) = angle(t, 2i+1) = t / 10000^(2i/dim)."""
+    positions = torch.arange(length, device=device, dtype=torch.float32)
+    exponents = torch.arange(0, dim, 2, device=device, dtype=torch.float32) / dim
+    angles = positions[:, None] * (1.0 / (10000 ** exponents))[None, :]
+    angles = angles.repeat_interleave(2, dim=-1)
+    return angles.cos().to(dtype), angles.sin().to(dtype)
+
+
+def apply_rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """x [B, N, H, C, D] with [C, D] tables (warpstate/model.py:45-49)."""
+    return x * cos + rotate_half(x) * sin
+
+
 class SwiGLU(nn.Module):
     """Packed projection: up in output columns [0, hidden), gate in [hidden, 2 hidden)."""
 
