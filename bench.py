@@ -329,6 +329,22 @@ def cpu_baseline(rows):
     return sum(flops_step(rows).values()) / sec / 1e12, sec, torch.get_num_threads()
 
 
+TRAFFIC_PROFILE = ROOT / "profiles" / "hbm_traffic_layer_step_m16384.md"
+
+
+def measured_traffic(region: str):
+    """HBM bytes per launch of a bench region, measured with rocprofv3 FETCH_SIZE and
+    WRITE_SIZE (scaled by a plain copy's readings) and recorded in the traffic profile;
+    None when the region has no measurement there."""
+    if not TRAFFIC_PROFILE.exists():
+        return None
+    for line in TRAFFIC_PROFILE.read_text().splitlines():
+        parts = line.split()
+        if len(parts) == 3 and parts[0] == "traffic_bytes" and parts[1] == region:
+            return int(parts[2])
+    return None
+
+
 def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -353,7 +369,7 @@ def main():
                 "achieved": round(dom["flops"] / dom["ms"] / 1e9, 1),
                 "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                 "frac": round(dom["flops"] / dom["ms"] / 1e9 / PEAK_BF16_TFLOPS, 4),
-                "traffic": None}
+                "traffic": measured_traffic(dom_name)}
     cpu = None
     if not args.no_cpu:
         tflops, sec, threads = cpu_baseline(args.cpu_rows)
