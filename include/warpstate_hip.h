@@ -132,16 +132,19 @@ int ws_swiglu_backward_mm(const void* grad, int64_t g_s0, int64_t g_s1, const vo
                           int64_t b_s0, int64_t b_s1, const void* packed, void* dpacked,
                           int64_t m, int64_t h, int64_t k, int eager_rounding, void* stream);
 
-/* Floats of the workspace ws_mm_accumulate_f32 needs for `splits` split-K slices
- * (0 when splits <= 1). */
-int64_t ws_mm_accumulate_workspace_floats(int64_t m, int64_t n, int64_t splits);
+/* Floats of the workspace ws_mm_accumulate_f32 needs for an [m, n] gradient with
+ * reduction k and `splits` (0 when splits <= 1), on the current device. */
+int64_t ws_mm_accumulate_workspace_floats(int64_t m, int64_t n, int64_t k, int64_t splits);
 
 /*
  * Weight-gradient GEMM accumulated into an FP32 buffer: G[m,n] += f32(r(A @ B)) when
  * round_bf16 (the BF16 dW then AccumulateGrad of test_gradient_execution.py:243-246 and
  * ops/matmul_execution.py:243), or G += A @ B in FP32 otherwise (the "direct_fp32_addmm"
- * variant of ops/benchmark_gradient_accumulation.py:141-144). splits > 1 reduces K in
- * slices through `workspace`.
+ * variant of ops/benchmark_gradient_accumulation.py:141-144). splits > 1 lets the
+ * reduction be split through `workspace`: for operands with a contiguous reduction or row
+ * dimension the 256 x 256 tiles that fill whole rounds of the GPU accumulate directly and
+ * the remaining tiles' k-range is shared evenly by all compute units (FP32 partial sums,
+ * added in k order, rounded once); other layouts use `splits` even k-slices.
  */
 int ws_mm_accumulate_f32(const void* a, int64_t a_s0, int64_t a_s1, const void* b, int64_t b_s0,
                          int64_t b_s1, float* g, int64_t ldg, int64_t m, int64_t n, int64_t k,

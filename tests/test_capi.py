@@ -45,8 +45,11 @@ def test_queries_without_device_work():
     lib = _hip.library()
     assert lib.ws_version().startswith(b"warpstate-hip")
     assert _hip.query("ws_linear_ce_parts", 32768) == 2 * 128
-    assert _hip.query("ws_mm_accumulate_workspace_floats", 10, 20, 1) == 0
-    assert _hip.query("ws_mm_accumulate_workspace_floats", 10, 20, 4) == 800
+    assert _hip.query("ws_mm_accumulate_workspace_floats", 10, 20, 64, 1) == 0
+    # At least the even slices; at least one 256 x 256 partial block per piece of the
+    # single (stream-K shared) tile.
+    assert _hip.query("ws_mm_accumulate_workspace_floats", 10, 20, 64, 4) >= 800
+    assert _hip.query("ws_mm_accumulate_workspace_floats", 10, 20, 64, 4) % 65536 == 0
     # One partial weight-gradient row per 64-row block.
     assert _hip.query("ws_rmsnorm_backward_partial_floats", 10, 64) == 64
     assert _hip.query("ws_rmsnorm_backward_partial_floats", 16384, 2048) == 256 * 2048

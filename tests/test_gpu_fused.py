@@ -162,6 +162,64 @@ def test_weight_gradient_fp32_accumulation(splits, layout):
     assert_f32_close(gg.cpu(), oracle.accumulate_weight_grad(g, a, b), f"{layout} splits={splits}")
 
 
+def test_balanced_accumulation_whole_rounds_plus_shared_tiles():
+    """272 output tiles on a 256-CU GPU: 256 run whole and accumulate directly, the last
+    tile row's k-range is shared by all CUs and summed from FP32 partials. Rows from both
+    regions match the oracle, and the whole buffer matches the unsplit path."""
+    from ops.fused_execution import mm_accumulate_
+
+    gen = _gen(77)
+    tokens, n_out, n_in = 1024, 17 * 256, 16 * 256
+    dy = torch.randn(tokens, n_out, generator=gen).bfloat16()
+    x = torch.randn(tokens, n_in, generator=gen).bfloat16()
+    g = torch.randn(n_out, n_in, generator=gen) * 1e-2
+    a, b = dy.cuda().T, x.cuda()
+    balanced, plain = g.cuda(), g.cuda()
+    mm_accumulate_(balanced, a, b, True, 2)
+    mm_accumulate_(plain, a, b, True, 1)
+    torch.cuda.synchronize()
+    rows = torch.cat([torch.arange(0, 64), torch.arange(16 * 256, 17 * 256)])
+    want = oracle.accumulate_weight_grad(g[rows], dy.T[rows], x)
+    assert_f32_close(balanced.cpu()[rows], want, "balanced, sampled rows")
+    assert_f32_close(balanced.cpu(), plain.cpu(), "balanced vs unsplit")
+
+
+@pytest.mark.parametrize("round_bf16", [True, False])
+def test_balanced_accumulation_ragged_tiles(round_bf16):
+    """The balanced split with ragged rows, columns and k: 17 x 16 tiles whose last row
+    and column of tiles are partial, 1000-long reduction (the last k-tile partial)."""
+    from ops.fused_execution import mm_accumulate_
+
+    gen = _gen(79)
+    tokens, n_out, n_in = 1000, 17 * 256 - 100, 16 * 256 - 36
+    dy = torch.randn(tokens, n_out, generator=gen).bfloat16()
+    x = torch.randn(tokens, n_in, generator=gen).bfloat16()
+    g = torch.randn(n_out, n_in, generator=gen) * 1e-2
+    balanced = g.cuda()
+    mm_accumulate_(balanced, dy.cuda().T, x.cuda(), round_bf16, 2)
+    torch.cuda.synchronize()
+    rows = torch.cat([torch.arange(0, 32), torch.arange(n_out - 200, n_out)])
+    want = oracle.accumulate_weight_grad(g[rows], dy.T[rows], x, round_bf16)
+    assert_f32_close(balanced.cpu()[rows], want, f"balanced ragged round={round_bf16}")
+
+
+@pytest.mark.parametrize("round_bf16", [True, False])
+def test_balanced_accumulation_ragged_edges(round_bf16):
+    """Ragged rows, columns and k (47 k-tiles, the last one partial) in even k-slices."""
+    from ops.fused_execution import mm_accumulate_
+
+    gen = _gen(78)
+    tokens, n_out, n_in = 3000, 300, 264
+    dy = torch.randn(tokens, n_out, generator=gen).bfloat16()
+    x = torch.randn(tokens, n_in, generator=gen).bfloat16()
+    g = torch.randn(n_out, n_in, generator=gen) * 1e-2
+    gg = g.cuda()
+    mm_accumulate_(gg, dy.cuda().T, x.cuda(), round_bf16, 2)
+    torch.cuda.synchronize()
+    assert_f32_close(gg.cpu(), oracle.accumulate_weight_grad(g, dy.T, x, round_bf16),
+                     f"ragged round={round_bf16}")
+
+
 def test_weight_gradient_zero_upstream_leaves_buffer_bitwise():
     from ops.fused_execution import mm_accumulate_
 

@@ -120,8 +120,74 @@ extern "C" int ws_swiglu_backward_mm(const void* grad, int64_t g_s0, int64_t g_s
       p, am, bm, LaunchCfg{0, 1}, s);
 }
 
-extern "C" int64_t ws_mm_accumulate_workspace_floats(int64_t m, int64_t n, int64_t splits) {
-  return splits <= 1 ? 0 : m * n * splits;
+namespace {
+
+// Balanced accumulation plan for an [m, n] output with k-reduction k on `workers` CUs:
+// whole rounds of 256 x 256 tiles run data-parallel, the other tiles' k-tiles are shared
+// evenly (stream-K) with at most `pieces` pieces per tile.
+struct BalancedPlan {
+  int tiles_m, tiles_n, tiles, k_tiles, dp_tiles, sk_tiles, pieces;
+  long units;
+  long workspace_floats() const { return (long)sk_tiles * pieces * kFBM * kFBN; }
+};
+
+BalancedPlan balanced_plan(long m, long n, long k, int workers) {
+  BalancedPlan b{};
+  b.tiles_m = cdiv(m, kFBM);
+  b.tiles_n = cdiv(n, kFBN);
+  b.tiles = b.tiles_m * b.tiles_n;
+  b.k_tiles = cdiv(k, kFBK);
+  b.dp_tiles = b.tiles / workers * workers;
+  b.sk_tiles = b.tiles - b.dp_tiles;
+  b.units = (long)b.sk_tiles * b.k_tiles;
+  b.pieces = 0;
+  for (long ti = 0; ti < b.sk_tiles; ++ti) {
+    const int pc = sk_pieces_of(ti, b.k_tiles, b.units, workers);
+    if (pc > b.pieces) b.pieces = pc;
+  }
+  return b;
+}
+
+// G[m, n] += f32(r(sum of the tile's pieces)) for the stream-K tiles of a balanced
+// accumulation: block (tile ti, chunk) handles 1024 elements of tile ti's 256 x 256 block,
+// four consecutive columns per thread; pieces are added in k order.
+__global__ void __launch_bounds__(256) sk_accum_kernel(const float* __restrict__ ws,
+                                                       float* __restrict__ g, long ldg, int M,
+                                                       int N, int tiles_m, int tiles_n,
+                                                       int dp_tiles, int k_tiles, long units,
+                                                       int workers, int pieces_max,
+                                                       int round_acc, int vec) {
+  const long ti = blockIdx.x / 64;
+  const int e = (blockIdx.x % 64) * 1024 + threadIdx.x * 4;
+  const int r = e / kFBN, c = e % kFBN;
+  int tm, tn;
+  tile_position(dp_tiles + (int)ti, tiles_m, tiles_n, tm, tn);
+  const int m = tm * kFBM + r, n = tn * kFBN + c;
+  if (m >= M || n >= N) return;
+  const int pieces = sk_pieces_of(ti, k_tiles, units, workers);
+  const float* src = ws + ti * pieces_max * (long)(kFBM * kFBN) + e;
+  f32x4_t s = *reinterpret_cast<const f32x4_t*>(src);
+  for (int q = 1; q < pieces; ++q) s += *reinterpret_cast<const f32x4_t*>(src + (long)q * kFBM * kFBN);
+  if (round_acc) {
+#pragma unroll
+    for (int d = 0; d < 4; ++d) s[d] = rbf16(s[d]);
+  }
+  float* dst = g + (long)m * ldg + n;
+  if (vec && n + 3 < N) {
+    *reinterpret_cast<f32x4_t*>(dst) = *reinterpret_cast<const f32x4_t*>(dst) + s;
+  } else {
+    for (int d = 0; d < 4 && n + d < N; ++d) dst[d] += s[d];
+  }
+}
+
+}  // namespace
+
+extern "C" int64_t ws_mm_accumulate_workspace_floats(int64_t m, int64_t n, int64_t k, int64_t splits) {
+  if (splits <= 1 || m < 1 || n < 1 || k < 1) return 0;
+  // Even split-K slices (any operand layout), or the balanced plan (vector layouts).
+  const long even = m * n * splits;
+  const long balanced = balanced_plan(m, n, k, device_cus()).workspace_floats();
+  return even > balanced ? even : balanced;
 }
 
 extern "C" int ws_mm_accumulate_f32(const void* a, int64_t a_s0, int64_t a_s1, const void* b,
@@ -139,20 +205,44 @@ extern "C" int ws_mm_accumulate_f32(const void* a, int64_t a_s0, int64_t a_s1, c
   p.M = (int)m; p.N = (int)n; p.K = (int)k;
   p.round_acc = round_bf16 ? 1 : 0;
   int am = operand_mode(p.a, m, k, 256), bm = operand_mode(p.b, n, k, 256);
+  p.g = g;
+  p.ldg = ldg;
+  p.vec_out = (n % 4 == 0) && (ldg % 4 == 0) && al(g, 16);
   if (splits <= 1) {
-    p.g = g;
-    p.ldg = ldg;
-    p.vec_out = (n % 4 == 0) && (ldg % 4 == 0) && al(g, 16);
     if (fast_ok(p, am, bm, false))
       return dispatch_fast<false, FEpiAccF32<false>>(p, am, bm, LaunchCfg{0, 1}, s);
     return dispatch<kMaskMM, WS_TILE_ARGS_LARGE, false, false, EpiAccF32<false>>(p, am, bm,
                                                                                   LaunchCfg{0, 1}, s);
   }
+  const int workers = device_cus();
+  const BalancedPlan plan = balanced_plan(m, n, k, workers);
+  const bool fast = fast_ok(p, am, bm, false);
+  if (fast && plan.sk_tiles == 0)  // whole rounds of tiles: nothing to split
+    return dispatch_fast<false, FEpiAccF32<false>>(p, am, bm, LaunchCfg{0, 1}, s);
+  if (fast && plan.dp_tiles > 0 && al(workspace, 16)) {
+    // Balanced: whole rounds of tiles accumulate directly, the rest is shared stream-K.
+    p.balanced = 1;
+    p.dp_tiles = plan.dp_tiles;
+    p.sk_tiles = plan.sk_tiles;
+    p.k_tiles = plan.k_tiles;
+    p.sk_units = plan.units;
+    p.sk_pieces = plan.pieces;
+    p.sk_ws = workspace;
+    if (int rc = dispatch_fast<false, FEpiAccF32<false>>(p, am, bm, LaunchCfg{1, 1, workers}, s))
+      return rc;
+    hipLaunchKernelGGL(sk_accum_kernel, dim3((unsigned)(plan.sk_tiles * 64)), dim3(256), 0, s,
+                       workspace, g, (long)ldg, (int)m, (int)n, plan.tiles_m, plan.tiles_n,
+                       plan.dp_tiles, plan.k_tiles, plan.units, workers, plan.pieces,
+                       round_bf16 ? 1 : 0, p.vec_out);
+    return hip_check(hipGetLastError(), "stream-K reduce launch");
+  }
+  // Fewer tiles than compute units, or generic layouts: even split-K slices through the
+  // workspace, then one reduction pass.
   p.g = workspace;
   p.ldg = n;
   p.split_stride = m * n;
   p.vec_out = (n % 4 == 0) && al(workspace, 16);
-  if (fast_ok(p, am, bm, false)) {
+  if (fast && p.vec_out) {
     if (int rc = dispatch_fast<false, FEpiAccF32<true>>(p, am, bm, LaunchCfg{0, (int)splits}, s))
       return rc;
   } else if (int rc = dispatch<kMaskMM, WS_TILE_ARGS_LARGE, false, false, EpiAccF32<true>>(

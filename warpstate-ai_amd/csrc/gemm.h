@@ -71,6 +71,14 @@ struct GemmParams {
   float* part_max; float* part_sum; float* tgt_logit; int parts_per_row;
   const float* grad_scale;  // device scalar: d(mean) / max(1, count)
   int row_offset;
+  // Balanced FP32 accumulation (fast kernel): tiles [0, dp_tiles) of the raster run whole
+  // and accumulate into g; the k-tiles of the other sk_tiles tiles (sk_units = sk_tiles x
+  // k_tiles in all) are shared evenly by the gridDim.x workgroups, each piece writing a
+  // 256 x 256 FP32 block (tile, piece) of sk_ws with at most sk_pieces pieces per tile.
+  int balanced;
+  int dp_tiles, sk_tiles, k_tiles, sk_pieces;
+  long sk_units;
+  float* sk_ws;
 };
 
 // --------------------------------------------------------------------------------------
@@ -84,6 +92,15 @@ __device__ __forceinline__ int xcd_remap(int w, int total, int window) {
   if (size % kXcds != 0) return w;
   int within = w - base;
   return base + (within % kXcds) * (size / kXcds) + within / kXcds;
+}
+
+// Stream-K shares: worker v of W owns units [sk_begin(v), sk_begin(v + 1)) of U.
+__host__ __device__ inline long sk_begin(long v, long U, long W) { return v * U / W; }
+// The worker whose share holds unit x (the largest v with sk_begin(v) <= x).
+__host__ __device__ inline long sk_worker(long x, long U, long W) { return ((x + 1) * W - 1) / U; }
+// Number of workers sharing stream-K tile ti (KT units per tile).
+__host__ __device__ inline int sk_pieces_of(long ti, long KT, long U, long W) {
+  return (int)(sk_worker((ti + 1) * KT - 1, U, W) - sk_worker(ti * KT, U, W) + 1);
 }
 
 // Grouped raster order of ops/matmul_kernels.py:72-78.

@@ -42,6 +42,7 @@ inline bool offsets_fit(int mode, long s_row, long s_k, int tile_rows) {
 struct LaunchCfg {
   int persistent;  // grid = resident workgroups instead of one per tile
   int splits;      // split-K slices (blockIdx.y)
+  int workers;     // > 0: exactly this many workgroups (balanced accumulation)
 };
 
 template <int BM, int BN, int WM, int WN, int AM, int BMD, bool PAIRED, bool RMS, class Epi>
@@ -128,6 +129,7 @@ int run_fast(GemmParams p, LaunchCfg cfg, hipStream_t stream) {
   const int resident = device_cus();
   dim3 grid(cfg.persistent ? (p.total_tiles < resident ? p.total_tiles : resident) : p.total_tiles,
             splits);
+  if (cfg.workers > 0) grid = dim3(cfg.workers, 1);
   hipLaunchKernelGGL((gemm_fast_kernel<AM, BMD, PAIRED, Epi>), grid, dim3(kFNT), kFLdsAlloc, stream, p);
   return hip_check(hipGetLastError(), "gemm launch");
 }

@@ -47,7 +47,7 @@ SIGNATURES = {
                               _c_void_p, _i64, _i64, _i64, _c_void_p]),
     "ws_swiglu_backward_mm": (_i32, [_c_void_p, _i64, _i64, _c_void_p, _i64, _i64, _c_void_p,
                                      _c_void_p, _i64, _i64, _i64, _i32, _c_void_p]),
-    "ws_mm_accumulate_workspace_floats": (_i64, [_i64, _i64, _i64]),
+    "ws_mm_accumulate_workspace_floats": (_i64, [_i64, _i64, _i64, _i64]),
     "ws_mm_accumulate_f32": (_i32, [_c_void_p, _i64, _i64, _c_void_p, _i64, _i64, _c_void_p, _i64,
                                     _i64, _i64, _i64, _i32, _c_void_p, _i64, _c_void_p]),
     "ws_linear_ce_parts": (_i64, [_i64]),

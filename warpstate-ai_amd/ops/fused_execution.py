@@ -190,8 +190,10 @@ def swiglu_backward_mm(grad: torch.Tensor, down_weight: torch.Tensor, packed: to
 def auto_splits(m: int, n: int, k: int, cus: int = 256, tile: int = 256,
                 max_splits: int = 4, min_k_tiles: int = 16) -> int:
     """Split-K factor for an [m, n] output with reduction k: the one (fewest on ties) that
-    fills the last round of 256 x 256 tiles on `cus` compute units best, keeping at least
-    `min_k_tiles` 64-wide k-tiles per split."""
+    fills the last round of 256 x 256 tiles on ``cus`` compute units best, keeping at
+    least ``min_k_tiles`` 64-wide k-tiles per split. With at least as many tiles as compute
+    units the library turns any factor above 1 into a balanced split (whole rounds of tiles
+    direct, the remaining tiles' k-range shared by all compute units)."""
     tiles = -(-m // tile) * -(-n // tile)
     best, best_eff = 1, 0.0
     for s in range(1, max_splits + 1):
@@ -208,8 +210,10 @@ def mm_accumulate_(g: torch.Tensor, a: torch.Tensor, b: torch.Tensor, round_bf16
                    splits: int | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
     """G += f32(r(a @ b)) (or G += a @ b in FP32 when ``round_bf16`` is False), in place.
 
-    G is FP32 [M, N] with unit column stride; ``splits`` > 1 splits the reduction through
-    an FP32 workspace of splits * M * N floats (None: chosen by ``auto_splits``)."""
+    G is FP32 [M, N] with unit column stride. ``splits`` > 1 lets the reduction be split
+    through an FP32 workspace (``ws_mm_accumulate_workspace_floats`` floats): balanced
+    stream-K shares for vector operand layouts, ``splits`` even slices otherwise (None:
+    chosen by ``auto_splits``)."""
     _check_bf16_cuda(a, b)
     if g.dtype != torch.float32 or g.stride(1) != 1:
         raise ValueError("Gradient buffer must be FP32 with unit column stride")
@@ -219,7 +223,7 @@ def mm_accumulate_(g: torch.Tensor, a: torch.Tensor, b: torch.Tensor, round_bf16
         raise ValueError("Gradient buffer shape must match a @ b")
     if splits is None:
         splits = auto_splits(m, n, k, torch.cuda.get_device_properties(g.device).multi_processor_count)
-    need = _hip.query("ws_mm_accumulate_workspace_floats", m, n, splits)
+    need = _hip.query("ws_mm_accumulate_workspace_floats", m, n, k, splits)
     if need and (workspace is None or workspace.numel() < need):
         workspace = torch.empty((need,), dtype=torch.float32, device=g.device)
     _hip.call("ws_mm_accumulate_f32", a.data_ptr(), a.stride(0), a.stride(1), b.data_ptr(),
