@@ -13,14 +13,16 @@
 //    as zeros.
 //  * K-contiguous operand tile: [rows][64 k], 128-byte rows of eight 16-byte chunks,
 //    chunk c of row r at slot c ^ swz(r) (gemm.h). Fragments are one ds_read_b128.
-//  * M/N-contiguous operand tile: [64 k][rows], 512-byte rows of 32 chunks (8 rows of
-//    the operand each), chunk c of k-row kk at slot c ^ 2 wtr(kk),
-//    wtr(kk) = (kk & 3) | ((kk >> 3 & 1) << 2). Fragments are two ds_read_b64_tr_b16:
-//    within each 16-lane group the transposing read hands element q of the 8 bytes
-//    addressed by lane L to lane 4 (L & 3) + q, slot L >> 2, so lane L addressing k-row
-//    k0 + (L >> 2), rows 4 (L & 3) .. + 3 leaves each lane four consecutive k of one row.
-//    The swizzle puts the four k-rows (and the next group's four) of one read on
-//    distinct 32-byte bank windows.
+//  * M/N-contiguous operand tile: four blocks of 64 operand rows, each [64 k][128 B]
+//    (8 KiB): chunk c (operand rows 8c .. 8c + 7 of the block) of k-row kk at slot
+//    c ^ mnsw(kk), mnsw(kk) = 2 ((kk >> 1 & 1) | (kk >> 3 & 1) << 1). A load instruction
+//    then covers 8 k-rows x 128 bytes, one cache line each (a [64 k][512 B] layout, with
+//    2 k-rows x 512 bytes per instruction, ran the weight gradients 7-10 % slower).
+//    Fragments are two ds_read_b64_tr_b16: within each 16-lane group the transposing read
+//    hands element q of the 8 bytes addressed by lane L to lane 4 (L & 3) + q, slot L >> 2,
+//    so lane L addressing k-row k0 + (L >> 2), rows 4 (L & 3) .. + 3 leaves each lane four
+//    consecutive k of one row. Per read the 16 k-rows x 32 bytes fall on 16 distinct
+//    16-byte bank slots twice each (two passes of 256 bytes, no conflicts).
 //  * MFMA v_mfma_f32_16x16x32_bf16 with the B fragment as the instruction's A operand:
 //    lane l then holds output row m = m0 + 16 i + (l & 15), columns n0 + 16 j + 4 (l >> 4)
 //    + e, e = 0..3, which the epilogues store as 8-byte (BF16) or 16-byte (FP32) vectors.
@@ -52,7 +54,7 @@ constexpr int kFIns = kFTileBytes / (kFNT * 16);         // 4 loads per thread p
 typedef float f32x4_v __attribute__((ext_vector_type(4)));
 typedef short i16x4_t __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ int wtr(int kk) { return (kk & 3) | (((kk >> 3) & 1) << 2); }
+__device__ __forceinline__ int mnsw(int kk) { return 2 * (((kk >> 1) & 1) | (((kk >> 3) & 1) << 1)); }
 
 // waitcnt immediate for "vmcnt <= n" leaving the other counters unconstrained (gfx9).
 constexpr int wait_vmcnt(int n) { return (n & 0xF) | (7 << 4) | (0xF << 8) | ((n >> 4) << 14); }
@@ -69,7 +71,7 @@ struct DmaTile {
   __device__ __forceinline__ static int k_of(int i, int wave, int lane) {
     const int byte = (i * (kFNT / kWave) + wave) * 1024 + lane * 16;
     if constexpr (MODE == kKContig) return 8 * (((byte >> 4) & 7) ^ swz(byte >> 7));
-    else return byte >> 9;
+    else return ((byte >> 10) & 7) * 8 + (lane >> 3);
   }
   __device__ __forceinline__ void init(const OperandDesc& d, int row0, int rows_valid, int half,
                                        int wave, int lane) {
@@ -82,8 +84,9 @@ struct DmaTile {
         const int phys = PAIRED && r >= 128 ? half + logical : logical;
         off[i] = logical < rows_valid ? (unsigned)((long)(phys - row0) * d.s_row * 2 + 16 * c) : kOOB;
       } else {
-        const int kk = byte >> 9, c = ((byte >> 4) & 31) ^ (2 * wtr(kk));
-        const int r = 8 * c;  // first operand row of the chunk
+        const int q = byte >> 10, kk = (q & 7) * 8 + (lane >> 3);
+        const int c = (lane & 7) ^ mnsw(kk);
+        const int r = (q >> 3) * 64 + 8 * c;  // first operand row of the chunk
         const int logical = row0 + (PAIRED && r >= 128 ? r - 128 : r);
         const int phys = PAIRED && r >= 128 ? half + logical : logical;
         off[i] = logical < rows_valid ? (unsigned)((phys - row0) * 2 + (long)kk * d.s_k * 2) : kOOB;
@@ -120,9 +123,9 @@ __device__ __forceinline__ bf16x8_t read_frag(const unsigned char* tile, int rb,
     const int m = rb + 4 * (L & 3);
     const int kk0 = 32 * s + 8 * g + (L >> 2);
     const int kk1 = kk0 + 4;
-    const int c = m >> 3, hb = (m & 4) * 2;  // byte within chunk: 0 or 8
-    const unsigned char* p0 = tile + kk0 * 512 + ((c ^ (2 * wtr(kk0))) << 4) + hb;
-    const unsigned char* p1 = tile + kk1 * 512 + ((c ^ (2 * wtr(kk1))) << 4) + hb;
+    const int blk = (m >> 6) * 8192, c = (m >> 3) & 7, hb = (m & 4) * 2;  // hb: 0 or 8
+    const unsigned char* p0 = tile + blk + kk0 * 128 + ((c ^ mnsw(kk0)) << 4) + hb;
+    const unsigned char* p1 = tile + blk + kk1 * 128 + ((c ^ mnsw(kk1)) << 4) + hb;
     i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
         (__attribute__((address_space(3))) i16x4_t*)(p0));
     i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
