@@ -102,13 +102,22 @@ struct DmaTile {
     const unsigned short* base =
         MODE == kKContig ? d.ptr + (long)row0 * d.s_row + k0 : d.ptr + row0 + (long)k0 * d.s_k;
     __amdgpu_buffer_rsrc_t rs = make_rsrc(base, 0x7fffffff);
-    const bool ragged = k0 + kFBK > K;
+    if (k0 + kFBK <= K) {
 #pragma unroll
-    for (int i = 0; i < kFIns; ++i) {
-      unsigned o = off[i];
-      if (ragged && k0 + k_of(i, wave, lane) >= K) o = kOOB;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, WS_LDS(lds_tile + (i * (kFNT / kWave) + wave) * 1024),
-                                               16, o, 0, 0, 0);
+      for (int i = 0; i < kFIns; ++i)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, WS_LDS(lds_tile + (i * (kFNT / kWave) + wave) * 1024),
+                                                 16, off[i], 0, 0, 0);
+    } else {
+      // Ragged last k-tile. The lane index goes through an empty asm so that the per-lane
+      // k offsets are computed here and not kept live across the k-loop.
+      int l = lane;
+      asm volatile("" : "+v"(l));
+#pragma unroll
+      for (int i = 0; i < kFIns; ++i) {
+        const unsigned o = k0 + k_of(i, wave, l) >= K ? kOOB : off[i];
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, WS_LDS(lds_tile + (i * (kFNT / kWave) + wave) * 1024),
+                                                 16, o, 0, 0, 0);
+      }
     }
   }
 };
@@ -143,6 +152,11 @@ struct Acc16 {
   f32x4_v v[FA][FB];
 };
 
+// The lane index through an empty asm: per-lane address math that depends on it stays in
+// the epilogue instead of being hoisted out of the tile loop and kept live (spilled)
+// across the main loop.
+__device__ __forceinline__ void opaque_lane(int& lane) { asm volatile("" : "+v"(lane)); }
+
 // --------------------------------------------------------------------------------------
 // Epilogues on the 16x16 accumulator layout. Lane l holds, for block (i, j), row
 //   m = m_base + 16 i + (l & 15) and columns n = n_base + 16 j + 4 (l >> 4) + e.
@@ -157,6 +171,7 @@ struct FEpiStore {
   __device__ __forceinline__ static void run(const GemmParams& p, Acc16<FA, FB>& acc, int m_base,
                                              int n_base, int lane, int tm, int tn, int wn,
                                              unsigned char* stage) {
+    opaque_lane(lane);
     const int m0 = tm * kFBM, n0 = tn * kFBN;
     unsigned short* cbase = p.c + (long)m0 * p.ldc + n0;
     __amdgpu_buffer_rsrc_t rc = make_rsrc(cbase, 0x7fffffff);
@@ -205,6 +220,7 @@ struct FEpiSwiglu {
   __device__ __forceinline__ static void run(const GemmParams& p, Acc16<FA, FB>& acc, int m_base,
                                              int n_base, int lane, int tm, int tn, int wn,
                                              unsigned char* stage) {
+    opaque_lane(lane);
     constexpr int FH = FB / 2;
     const int m0 = tm * kFBM, n0 = tn * (kFBN / 2);
     unsigned short* pbase = p.c + (long)m0 * p.ldc + n0;
@@ -263,6 +279,7 @@ struct FEpiSwigluBwd {
   __device__ __forceinline__ static void run(const GemmParams& p, Acc16<FA, FB>& acc, int m_base,
                                              int n_base, int lane, int tm, int tn, int wn,
                                              unsigned char* stage) {
+    opaque_lane(lane);
     const long hoff = p.H;
     {
       // Fragment order -> staging rows (64 x 128 BF16, 272-byte rows).
@@ -284,18 +301,23 @@ struct FEpiSwigluBwd {
       // Buffer bases at this wave's tile origin keep the byte offsets small.
       __amdgpu_buffer_rsrc_t rp = make_rsrc(p.aux + (long)m_base * p.ldaux + n_base, 0x7fffffff);
       __amdgpu_buffer_rsrc_t rd = make_rsrc(p.c + (long)m_base * p.ldc + n_base, 0x7fffffff);
+      // All 16 rows' saved up/gate values are requested first (128 VGPRs; the
+      // accumulators are dead once staged), so the four row groups below wait for one
+      // memory latency instead of four.
+      u32x4_t vu[4][4], vg[4][4];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        u32x4_t vu[4], vg[4];
+      for (int q = 0; q < 4; ++q)
 #pragma unroll
         for (int h = 0; h < 4; ++h) {
           const int r = 16 * q + 4 * h + (lane >> 4);
           const int m = m_base + r;
           const bool ok = m < p.M && n + 7 < p.N;
           const long off = (long)r * p.ldaux + c8;
-          vu[h] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rp, store_off(ok, off, 2), 0, 0));
-          vg[h] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rp, store_off(ok, off + hoff, 2), 0, 0));
+          vu[q][h] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rp, store_off(ok, off, 2), 0, 0));
+          vg[q][h] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rp, store_off(ok, off + hoff, 2), 0, 0));
         }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
 #pragma unroll
         for (int h = 0; h < 4; ++h) {
           const int r = 16 * q + 4 * h + (lane >> 4);
@@ -306,8 +328,8 @@ struct FEpiSwigluBwd {
 #pragma unroll
           for (int d = 0; d < 4; ++d) {
             float du0, dg0, du1, dg1;
-            math(p, lo_bf16(vd[d]), lo_bf16(vu[h][d]), lo_bf16(vg[h][d]), du0, dg0);
-            math(p, hi_bf16(vd[d]), hi_bf16(vu[h][d]), hi_bf16(vg[h][d]), du1, dg1);
+            math(p, lo_bf16(vd[d]), lo_bf16(vu[q][h][d]), lo_bf16(vg[q][h][d]), du0, dg0);
+            math(p, hi_bf16(vd[d]), hi_bf16(vu[q][h][d]), hi_bf16(vg[q][h][d]), du1, dg1);
             od[d] = pack_bf16x2(du0, du1);
             og[d] = pack_bf16x2(dg0, dg1);
           }
@@ -315,7 +337,6 @@ struct FEpiSwigluBwd {
           __builtin_amdgcn_raw_buffer_store_b128(od, rd, store_off(ok, off, 2), 0, 0);
           __builtin_amdgcn_raw_buffer_store_b128(og, rd, store_off(ok, off + hoff, 2), 0, 0);
         }
-        __builtin_amdgcn_sched_barrier(0);
       }
     }
   }
@@ -328,6 +349,7 @@ struct FEpiAccF32 {
   __device__ __forceinline__ static void run(const GemmParams& p, Acc16<FA, FB>& acc, int m_base,
                                              int n_base, int lane, int tm, int tn, int wn,
                                              unsigned char* stage) {
+    opaque_lane(lane);
     const int m0 = tm * kFBM, n0 = tn * kFBN;
     float* gbase = p.g + (SPLIT ? (long)blockIdx.y * p.split_stride : 0) + (long)m0 * p.ldg + n0;
     __amdgpu_buffer_rsrc_t rg = make_rsrc(gbase, 0x7fffffff);
@@ -364,6 +386,7 @@ struct FEpiPartial {
   template <int FA, int FB>
   __device__ __forceinline__ static void run(Acc16<FA, FB>& acc, int r0, int c0, int lane,
                                              float* block) {
+    opaque_lane(lane);
 #pragma unroll
     for (int i = 0; i < FA; ++i) {
       const int r = r0 + 16 * i + (lane & 15);
@@ -384,6 +407,7 @@ struct FEpiCEStats {
   __device__ __forceinline__ static void run(const GemmParams& p, Acc16<FA, FB>& acc, int m_base,
                                              int n_base, int lane, int tm, int tn, int wn,
                                              unsigned char* stage) {
+    opaque_lane(lane);
     const int part = tn * kFWN + wn;
 #pragma unroll
     for (int i = 0; i < FA; ++i) {
@@ -427,6 +451,7 @@ struct FEpiCEGrad {
   __device__ __forceinline__ static void run(const GemmParams& p, Acc16<FA, FB>& acc, int m_base,
                                              int n_base, int lane, int tm, int tn, int wn,
                                              unsigned char* stage) {
+    opaque_lane(lane);
     const int m0 = tm * kFBM, n0 = tn * kFBN;
     unsigned short* cbase = p.c + (long)m0 * p.ldc + n0;
     __amdgpu_buffer_rsrc_t rc = make_rsrc(cbase, 0x7fffffff);
