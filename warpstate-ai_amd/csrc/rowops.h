@@ -131,7 +131,7 @@ static __global__ void __launch_bounds__(256) rmsnorm_fwd_kernel(const unsigned 
 // 8 l + 512 s (s < SEGS), and keeps its x and dy chunks in registers between the two
 // passes over the row. A block of 4 waves takes kRmsRowsPerBlock consecutive rows and writes
 // one partial weight-gradient row (summed across its waves in LDS).
-constexpr int kRmsRowsPerBlock = 64;
+constexpr int kRmsRowsPerBlock = 32;
 
 template <int SEGS>
 static __global__ void __launch_bounds__(256) rmsnorm_bwd_kernel(
@@ -156,16 +156,27 @@ static __global__ void __launch_bounds__(256) rmsnorm_bwd_kernel(
     for (int e = 0; e < 8; ++e) part[s][e] = 0.0f;
 
   const int row_end = min(rows, (blockIdx.x + 1) * kRmsRowsPerBlock);
-  for (int row = blockIdx.x * kRmsRowsPerBlock + wave; row < row_end; row += 4) {
-    const float r = rstd[row];
-    u32x4_t xv[SEGS], gv[SEGS];
-    float dr = 0.0f;
+  // One row ahead: the next row's x and dy are requested before this row's reduction.
+  auto load = [&](int row, u32x4_t (&xv)[SEGS], u32x4_t (&gv)[SEGS]) {
 #pragma unroll
     for (int s = 0; s < SEGS; ++s) {
       const int c = 8 * lane + 512 * s;
-      const bool ok = c < D;
+      const bool ok = c < D && row < row_end;
       xv[s] = ok ? *reinterpret_cast<const u32x4_t*>(x + (long)row * D + c) : u32x4_t{0u, 0u, 0u, 0u};
       gv[s] = ok ? *reinterpret_cast<const u32x4_t*>(dy + (long)row * D + c) : u32x4_t{0u, 0u, 0u, 0u};
+    }
+  };
+  u32x4_t xn[SEGS], gn[SEGS];
+  load(blockIdx.x * kRmsRowsPerBlock + wave, xn, gn);
+  for (int row = blockIdx.x * kRmsRowsPerBlock + wave; row < row_end; row += 4) {
+    const float r = rstd[row];
+    u32x4_t xv[SEGS], gv[SEGS];
+#pragma unroll
+    for (int s = 0; s < SEGS; ++s) { xv[s] = xn[s]; gv[s] = gn[s]; }
+    load(row + 4, xn, gn);
+    float dr = 0.0f;
+#pragma unroll
+    for (int s = 0; s < SEGS; ++s) {
 #pragma unroll
       for (int d = 0; d < 4; ++d) {
         float dz0 = lo_bf16(gv[s][d]) * wb[s][2 * d], dz1 = hi_bf16(gv[s][d]) * wb[s][2 * d + 1];
