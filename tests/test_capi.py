@@ -52,7 +52,7 @@ def test_queries_without_device_work():
     assert _hip.query("ws_mm_accumulate_workspace_floats", 10, 20, 64, 4) % 65536 == 0
     # One partial weight-gradient row per 64-row block.
     assert _hip.query("ws_rmsnorm_backward_partial_floats", 10, 64) == 64
-    assert _hip.query("ws_rmsnorm_backward_partial_floats", 16384, 2048) == 256 * 2048
+    assert _hip.query("ws_rmsnorm_backward_partial_floats", 16384, 2048) == 512 * 2048
     # One 4096-row chunk of BF16 logit gradients plus two FP32 dHidden partial slices.
     assert _hip.query("ws_linear_ce_workspace_bytes", 16384, 32768, 2048, 4096) == \
         256 + 4096 * 32768 * 2 + 2 * 4096 * 2048 * 4
