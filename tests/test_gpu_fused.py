@@ -104,6 +104,36 @@ def test_residual_projection(m, ffn, d):
                       "residual")
 
 
+@pytest.mark.parametrize("m,ffn,d", [(128, 384, 260), (264, 512, 516)])
+def test_residual_projection_width_4_mod_8(m, ffn, d):
+    """Output widths with N % 8 == 4: the staged epilogue writes the last 4 columns of a
+    row as a half (8-byte) piece and reads the residual the same way."""
+    from ops.benchmark_configs import down_residual_inputs
+    from ops.fused_execution import residual_mm
+
+    inp = down_residual_inputs(m=m, ffn=ffn, d=d, seed=3)
+    out = residual_mm(inp["h"].cuda(), inp["w_down"].cuda(), inp["residual"].cuda())
+    torch.cuda.synchronize()
+    assert_bf16_close(out, oracle.residual_projection(inp["h"], inp["w_down"], inp["residual"]),
+                      "residual N % 8 == 4")
+    zero = residual_mm(inp["h"].cuda(), torch.zeros_like(inp["w_down"]).cuda(), inp["residual"].cuda())
+    torch.cuda.synchronize()
+    assert torch.equal(zero.cpu(), inp["residual"])
+
+
+def test_rmsnorm_gate_projection_width_4_mod_8():
+    from ops.benchmark_configs import rms_projection_inputs
+    from ops.fused_execution import rmsnorm_gate_mm
+
+    gate = (256, 388)
+    inp = rms_projection_inputs(m=200, d=256, n=516, gate=gate, seed=5)
+    out, _ = rmsnorm_gate_mm(inp["x"].cuda(), inp["norm_weight"].cuda(), inp["eps"],
+                             inp["w"].cuda(), gate)
+    torch.cuda.synchronize()
+    want = oracle.rmsnorm_gate_projection(inp["x"], inp["norm_weight"], inp["eps"], inp["w"], gate)
+    assert_bf16_close(out, want, "rms gate projection N % 8 == 4")
+
+
 def test_residual_zero_weight_returns_residual_bitwise():
     from ops.fused_execution import residual_mm
 

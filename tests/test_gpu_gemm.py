@@ -43,7 +43,8 @@ def test_odd_shapes_and_transposed_operands(algorithm, layouts, tile):
 
 
 @pytest.mark.parametrize("layouts", LAYOUTS)
-@pytest.mark.parametrize("shape", [(256, 384, 512), (520, 264, 200), (1024, 2048, 1024)])
+@pytest.mark.parametrize("shape", [(256, 384, 512), (520, 264, 200), (1024, 2048, 1024),
+                                   (264, 260, 136), (300, 516, 256)])
 @pytest.mark.parametrize("tile", [(128, 128, 32, 4, 3), (64, 64, 32, 4, 3)])
 def test_aligned_shapes_vector_loaders(layouts, shape, tile):
     from ops.matmul_kernels import launch_mm

@@ -164,50 +164,78 @@ __device__ __forceinline__ void opaque_lane(int& lane) { asm volatile("" : "+v"(
 // without vector outputs to the generic kernel of gemm.h.
 
 // Plain BF16 store with optional column-range sigmoid and BF16 residual add
-// (same numerics as EpiStore).
+// (same numerics as EpiStore). The wave's 64 x 128 tile goes through its LDS staging rows
+// so that the global writes (and residual reads) are 16-byte pieces covering 256 bytes
+// of each row, instead of 8-byte pieces scattered over 16 rows per instruction.
 template <bool SIGMOID, bool RESIDUAL>
 struct FEpiStore {
   template <int FA, int FB>
   __device__ __forceinline__ static void run(const GemmParams& p, Acc16<FA, FB>& acc, int m_base,
                                              int n_base, int lane, int tm, int tn, int wn,
                                              unsigned char* stage) {
+    static_assert(FA * 16 == 64 && FB * 16 == 128, "staging holds a 64 x 128 wave tile");
     opaque_lane(lane);
-    const int m0 = tm * kFBM, n0 = tn * kFBN;
-    unsigned short* cbase = p.c + (long)m0 * p.ldc + n0;
-    __amdgpu_buffer_rsrc_t rc = make_rsrc(cbase, 0x7fffffff);
-    const unsigned short* rbase = RESIDUAL ? p.aux + (long)m0 * p.ldaux + n0 : cbase;
-    __amdgpu_buffer_rsrc_t rr = make_rsrc(rbase, 0x7fffffff);
+    // Fragment order -> staging rows, sigmoid applied, every value rounded to BF16.
 #pragma unroll
-    for (int i = 0; i < FA; ++i) {
-      const int m = m_base + 16 * i + (lane & 15);
-      const bool mok = m < p.M;
+    for (int i = 0; i < FA; ++i)
 #pragma unroll
       for (int j = 0; j < FB; ++j) {
-        const int n = n_base + 16 * j + 4 * (lane >> 4);
+        const int r = 16 * i + (lane & 15), c = 16 * j + 4 * (lane >> 4);
         float v[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           float x = acc.v[i][j][e];
           if (SIGMOID) {
             x = rbf16(x);
-            if (n + e >= p.gate_lo && n + e < p.gate_hi) x = sigmoid(x);
+            const int n = n_base + c + e;
+            if (n >= p.gate_lo && n < p.gate_hi) x = sigmoid(x);
           }
           v[e] = x;
         }
-        {
-          const bool ok = mok && (n + 3 < p.N);
-          if (RESIDUAL) {
-            u32x2_t rv = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(
-                rr, store_off(ok, (long)(m - m0) * p.ldaux + (n - n0), 2), 0, 0));
-            v[0] = rbf16(v[0]) + lo_bf16(rv[0]);
-            v[1] = rbf16(v[1]) + hi_bf16(rv[0]);
-            v[2] = rbf16(v[2]) + lo_bf16(rv[1]);
-            v[3] = rbf16(v[3]) + hi_bf16(rv[1]);
-          }
-          u32x2_t out = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
-          __builtin_amdgcn_raw_buffer_store_b64(out, rc,
-                                                store_off(ok, (long)(m - m0) * p.ldc + (n - n0), 2), 0, 0);
+        u32x2_t w = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+        *reinterpret_cast<u32x2_t*>(stage + r * kFStageRow + c * 2) = w;
+      }
+    // The accumulators are dead from here; the loads below must not be hoisted above.
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's staging writes landed
+    // Row order: lane (16 per row) owns 8 columns; 4 rows per instruction.
+    const int c8 = 8 * (lane & 15);
+    const int n = n_base + c8;
+    const bool full = n + 7 < p.N, half = n + 3 < p.N;  // N % 4 == 0 (vec_out)
+    __amdgpu_buffer_rsrc_t rc = make_rsrc(p.c + (long)m_base * p.ldc + n_base, 0x7fffffff);
+    u32x4_t rv[16];
+    if (RESIDUAL) {
+      __amdgpu_buffer_rsrc_t rr = make_rsrc(p.aux + (long)m_base * p.ldaux + n_base, 0x7fffffff);
+#pragma unroll
+      for (int q = 0; q < 16; ++q) {
+        const int r = 4 * q + (lane >> 4);
+        const bool ok = m_base + r < p.M;
+        const long off = (long)r * p.ldaux + c8;
+        if (full) {
+          rv[q] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rr, store_off(ok, off, 2), 0, 0));
+        } else {
+          const u32x2_t h = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(
+              rr, store_off(ok && half, off, 2), 0, 0));
+          rv[q] = u32x4_t{h[0], h[1], 0u, 0u};
         }
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      const int r = 4 * q + (lane >> 4);
+      const bool ok = m_base + r < p.M;
+      u32x4_t vd = *reinterpret_cast<const u32x4_t*>(stage + r * kFStageRow + c8 * 2);
+      if (RESIDUAL) {
+#pragma unroll
+        for (int d = 0; d < 4; ++d)
+          vd[d] = pack_bf16x2(lo_bf16(vd[d]) + lo_bf16(rv[q][d]), hi_bf16(vd[d]) + hi_bf16(rv[q][d]));
+      }
+      const long off = (long)r * p.ldc + c8;
+      if (full) {
+        __builtin_amdgcn_raw_buffer_store_b128(vd, rc, store_off(ok, off, 2), 0, 0);
+      } else {
+        const u32x2_t h = {vd[0], vd[1]};
+        __builtin_amdgcn_raw_buffer_store_b64(h, rc, store_off(ok && half, off, 2), 0, 0);
       }
     }
   }
