@@ -242,47 +242,57 @@ struct FEpiStore {
 };
 
 // Paired SwiGLU forward (EpiSwiglu numerics): blocks j < FB/2 are up columns, j + FB/2
-// the gate columns of the same output columns.
+// the gate columns of the same output columns. The rounded up | gate tile goes through the
+// wave's LDS staging rows (64 rows x 64 up + 64 gate columns); then each lane takes 8
+// columns of one row, computes their activations and writes up, gate and activation as
+// 16-byte pieces (8 lanes per 128-byte row piece, 8 rows per instruction).
 struct FEpiSwiglu {
   template <int FA, int FB>
   __device__ __forceinline__ static void run(const GemmParams& p, Acc16<FA, FB>& acc, int m_base,
                                              int n_base, int lane, int tm, int tn, int wn,
                                              unsigned char* stage) {
+    static_assert(FA * 16 == 64 && FB * 16 == 128, "staging holds a 64 x 128 wave tile");
     opaque_lane(lane);
-    constexpr int FH = FB / 2;
-    const int m0 = tm * kFBM, n0 = tn * (kFBN / 2);
-    unsigned short* pbase = p.c + (long)m0 * p.ldc + n0;
-    unsigned short* abase = p.c2 + (long)m0 * p.ldc2 + n0;
-    __amdgpu_buffer_rsrc_t rp = make_rsrc(pbase, 0x7fffffff);
-    __amdgpu_buffer_rsrc_t ra = make_rsrc(abase, 0x7fffffff);
+#pragma unroll
+    for (int i = 0; i < FA; ++i)
+#pragma unroll
+      for (int j = 0; j < FB; ++j) {
+        const int r = 16 * i + (lane & 15), c = 16 * j + 4 * (lane >> 4);
+        u32x2_t w = {pack_bf16x2(acc.v[i][j][0], acc.v[i][j][1]),
+                     pack_bf16x2(acc.v[i][j][2], acc.v[i][j][3])};
+        *reinterpret_cast<u32x2_t*>(stage + r * kFStageRow + c * 2) = w;
+      }
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's staging writes landed
+    const int c8 = 8 * (lane & 7);
+    const int n = n_base + c8;  // column in [0, H)
+    const bool full = n + 7 < p.H, half = n + 3 < p.H;  // H % 4 == 0 (vec_out)
+    __amdgpu_buffer_rsrc_t rp = make_rsrc(p.c + (long)m_base * p.ldc + n_base, 0x7fffffff);
+    __amdgpu_buffer_rsrc_t ra = make_rsrc(p.c2 + (long)m_base * p.ldc2 + n_base, 0x7fffffff);
     const long hoff = p.H;
 #pragma unroll
-    for (int i = 0; i < FA; ++i) {
-      const int m = m_base + 16 * i + (lane & 15);
-      const bool mok = m < p.M;
+    for (int q = 0; q < 8; ++q) {
+      const int r = 8 * q + (lane >> 3);
+      const bool ok = m_base + r < p.M;
+      const u32x4_t vu = *reinterpret_cast<const u32x4_t*>(stage + r * kFStageRow + c8 * 2);
+      const u32x4_t vg = *reinterpret_cast<const u32x4_t*>(stage + r * kFStageRow + (64 + c8) * 2);
+      u32x4_t va;
 #pragma unroll
-      for (int j = 0; j < FH; ++j) {
-        const int n = n_base + 16 * j + 4 * (lane >> 4);
-        float up[4], gate[4], act[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          up[e] = rbf16(acc.v[i][j][e]);
-          gate[e] = rbf16(acc.v[i][j + FH][e]);
-          float s = silu(gate[e]);
-          if (p.eager) s = rbf16(s);
-          act[e] = s * up[e];
-        }
-        {
-          const bool ok = mok && (n + 3 < p.H);
-          const long rowp = (long)(m - m0) * p.ldc + (n - n0);
-          u32x2_t vu = {pack_bf16x2(up[0], up[1]), pack_bf16x2(up[2], up[3])};
-          u32x2_t vg = {pack_bf16x2(gate[0], gate[1]), pack_bf16x2(gate[2], gate[3])};
-          u32x2_t va = {pack_bf16x2(act[0], act[1]), pack_bf16x2(act[2], act[3])};
-          __builtin_amdgcn_raw_buffer_store_b64(vu, rp, store_off(ok, rowp, 2), 0, 0);
-          __builtin_amdgcn_raw_buffer_store_b64(vg, rp, store_off(ok, rowp + hoff, 2), 0, 0);
-          __builtin_amdgcn_raw_buffer_store_b64(
-              va, ra, store_off(ok, (long)(m - m0) * p.ldc2 + (n - n0), 2), 0, 0);
-        }
+      for (int d = 0; d < 4; ++d) {
+        float s0 = silu(lo_bf16(vg[d])), s1 = silu(hi_bf16(vg[d]));
+        if (p.eager) { s0 = rbf16(s0); s1 = rbf16(s1); }
+        va[d] = pack_bf16x2(s0 * lo_bf16(vu[d]), s1 * hi_bf16(vu[d]));
+      }
+      const long po = (long)r * p.ldc + c8, ao = (long)r * p.ldc2 + c8;
+      if (full) {
+        __builtin_amdgcn_raw_buffer_store_b128(vu, rp, store_off(ok, po, 2), 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b128(vg, rp, store_off(ok, po + hoff, 2), 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b128(va, ra, store_off(ok, ao, 2), 0, 0);
+      } else {
+        const bool okh = ok && half;
+        __builtin_amdgcn_raw_buffer_store_b64(u32x2_t{vu[0], vu[1]}, rp, store_off(okh, po, 2), 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b64(u32x2_t{vg[0], vg[1]}, rp, store_off(okh, po + hoff, 2), 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b64(u32x2_t{va[0], va[1]}, ra, store_off(okh, ao, 2), 0, 0);
       }
     }
   }
