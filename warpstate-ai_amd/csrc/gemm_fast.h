@@ -484,37 +484,53 @@ struct FEpiCEStats {
 };
 
 // LM-head pass 2 (EpiCEGrad numerics): r(scale * (softmax - onehot)), 0 for ignored rows.
+// The rounded logits go through the wave's LDS staging rows; each lane then takes 8
+// columns of one row (16 lanes per 256-byte row piece, 4 rows per instruction) and writes
+// 16-byte pieces.
 struct FEpiCEGrad {
   template <int FA, int FB>
   __device__ __forceinline__ static void run(const GemmParams& p, Acc16<FA, FB>& acc, int m_base,
                                              int n_base, int lane, int tm, int tn, int wn,
                                              unsigned char* stage) {
+    static_assert(FA * 16 == 64 && FB * 16 == 128, "staging holds a 64 x 128 wave tile");
     opaque_lane(lane);
-    const int m0 = tm * kFBM, n0 = tn * kFBN;
-    unsigned short* cbase = p.c + (long)m0 * p.ldc + n0;
-    __amdgpu_buffer_rsrc_t rc = make_rsrc(cbase, 0x7fffffff);
 #pragma unroll
-    for (int i = 0; i < FA; ++i) {
-      const int m = m_base + 16 * i + (lane & 15);
-      const bool mok = m < p.M;
-      const long tgt = mok ? p.targets[m] : -100;
-      const float lse = mok ? p.lse[m] : 0.0f;
-      const float scale = (tgt == -100) ? 0.0f : *p.grad_scale;
+    for (int i = 0; i < FA; ++i)
 #pragma unroll
       for (int j = 0; j < FB; ++j) {
-        const int n = n_base + 16 * j + 4 * (lane >> 4);
-        float v[4];
+        const int r = 16 * i + (lane & 15), c = 16 * j + 4 * (lane >> 4);
+        u32x2_t w = {pack_bf16x2(acc.v[i][j][0], acc.v[i][j][1]),
+                     pack_bf16x2(acc.v[i][j][2], acc.v[i][j][3])};
+        *reinterpret_cast<u32x2_t*>(stage + r * kFStageRow + c * 2) = w;
+      }
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's staging writes landed
+    const int c8 = 8 * (lane & 15);
+    const int n = n_base + c8;
+    const bool full = n + 7 < p.N, half = n + 3 < p.N;  // N % 4 == 0 (vec_out)
+    __amdgpu_buffer_rsrc_t rc = make_rsrc(p.c + (long)m_base * p.ldc + n_base, 0x7fffffff);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float l = rbf16(acc.v[i][j][e]);
-          v[e] = scale * exp_e(l - lse) - ((long)(n + e) == tgt ? scale : 0.0f);
-        }
-        {
-          const bool ok = mok && (n + 3 < p.N);
-          u32x2_t out = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
-          __builtin_amdgcn_raw_buffer_store_b64(out, rc,
-                                                store_off(ok, (long)(m - m0) * p.ldc + (n - n0), 2), 0, 0);
-        }
+    for (int q = 0; q < 16; ++q) {
+      const int r = 4 * q + (lane >> 4);
+      const int m = m_base + r;
+      const bool ok = m < p.M;
+      const long tgt = ok ? p.targets[m] : -100;
+      const float lse = ok ? p.lse[m] : 0.0f;
+      const float scale = (tgt == -100) ? 0.0f : *p.grad_scale;
+      const u32x4_t vl = *reinterpret_cast<const u32x4_t*>(stage + r * kFStageRow + c8 * 2);
+      u32x4_t o;
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        const long e = n + 2 * d;
+        const float v0 = scale * exp_e(lo_bf16(vl[d]) - lse) - (e == tgt ? scale : 0.0f);
+        const float v1 = scale * exp_e(hi_bf16(vl[d]) - lse) - (e + 1 == tgt ? scale : 0.0f);
+        o[d] = pack_bf16x2(v0, v1);
+      }
+      const long off = (long)r * p.ldc + c8;
+      if (full) {
+        __builtin_amdgcn_raw_buffer_store_b128(o, rc, store_off(ok, off, 2), 0, 0);
+      } else {
+        __builtin_amdgcn_raw_buffer_store_b64(u32x2_t{o[0], o[1]}, rc, store_off(ok && half, off, 2), 0, 0);
       }
     }
   }
