@@ -140,7 +140,7 @@ def prepare_layout(inputs: LayoutInputs, algorithm="paired", *, block=512, warps
     (ops/backward_layout.py:213-270).
 
     ``block`` and ``warps`` keep the reference's accepted values; on gfx950 the kernel's
-    work split is fixed (one 256-thread workgroup per head and block of up to 128 tokens),
+    work split is fixed (one 256-thread workgroup per head and block of up to 16 tokens),
     so they do not change the launch. The three algorithms give identical bits: "single"
     is one pass, "paired" a q/k pass then a v/gate/u pass, and "profile" the reference's
     two-kernel baseline that round-trips q and the key's rotated half-term through two
