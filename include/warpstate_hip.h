@@ -5,8 +5,9 @@
  * hipStream_t to launch on (passed as void*; from Python it is
  * torch.cuda.current_stream().cuda_stream of the calling thread). The library launches
  * work on that stream and returns; it never allocates, frees or synchronises. The caller
- * allocates every output and workspace. Outputs must not alias inputs; the FP32
- * gradient buffer of ws_mm_accumulate_f32 is the only in-place operand.
+ * allocates every output and workspace. Outputs must not alias inputs, except the FP32
+ * gradient buffer of ws_mm_accumulate_f32 (updated in place) and the output of
+ * ws_sigmoid_backward_cols (which may be its dout).
  *
  * Return value: 0 on success, 1 for an invalid argument (nothing was launched), 2 for a
  * HIP runtime error. ws_last_error() returns the calling thread's last message.
