@@ -14,7 +14,8 @@ def test_tuner_writes_results_and_a_loadable_policy(kind, monkeypatch):
     from ops import tune_matmul
     from ops.matmul_execution import matmul_plan_from_dict
 
-    scratch = tune_matmul.WORKSPACE / "gpurun_out" / "tuner-scratch"
+    # The tuner requires its temporary and cache directories inside the workspace.
+    scratch = tune_matmul.PACKAGE / "work" / f"tuner-scratch-{uuid.uuid4().hex[:8]}"
     scratch.mkdir(parents=True, exist_ok=True)
     monkeypatch.setenv("TMPDIR", str(scratch))
     monkeypatch.setenv("XDG_CACHE_HOME", str(scratch))
@@ -40,3 +41,4 @@ def test_tuner_writes_results_and_a_loadable_policy(kind, monkeypatch):
         assert all(entry.kind == kind for entry in plan.entries)
     finally:
         shutil.rmtree(out, ignore_errors=True)
+        shutil.rmtree(scratch, ignore_errors=True)
