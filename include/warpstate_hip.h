@@ -12,6 +12,12 @@
  * Return value: 0 on success, 1 for an invalid argument (nothing was launched), 2 for a
  * HIP runtime error. ws_last_error() returns the calling thread's last message.
  *
+ * Size limits: sizes are positive 32-bit integers. Kernels address a 256-row output tile
+ * with 32-bit offsets from the tile's first row, so 256 rows of every output must span
+ * less than 2 GiB (a BF16 row stride below 4,194,303 elements, an FP32 one below
+ * 2,097,151); wider outputs are rejected with status 1. Operands past the corresponding
+ * bound take a slower loader with 64-bit addresses instead.
+ *
  * Numerics: BF16 operands, FP32 accumulation in MFMA, BF16 round-to-nearest-even
  * outputs, at the rounding points of the reference's PyTorch path.
  *

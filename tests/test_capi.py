@@ -66,3 +66,9 @@ def test_invalid_arguments_are_rejected_before_any_launch():
         _hip.call("ws_mm", 16, 8, 1, 16, 8, 1, 16, 8, 8, 8, 7, 0, None)
     with pytest.raises(RuntimeError, match="gate column range"):
         _hip.call("ws_rmsnorm_gate_mm", 16, 8, 16, 1e-6, 16, 16, 16, 1, 8, 16, 8, 8, 8, 6, 9, None)
+    # A 256-row tile of the output must span less than 2 GiB (32-bit tile offsets).
+    with pytest.raises(RuntimeError, match="row stride"):
+        _hip.call("ws_mm", 16, 8, 1, 16, 8, 1, 16, 16, 4_200_000, 8, 0, 0, None)
+    with pytest.raises(RuntimeError, match="row stride"):
+        _hip.call("ws_mm_accumulate_f32", 16, 8, 1, 16, 8, 1, 16, 2_100_000, 16, 8, 8, 1, None,
+                  1, None)

@@ -98,6 +98,12 @@ extern "C" int ws_linear_ce_backward(const void* hidden, int64_t ld_hidden, cons
   if (ld_dhidden < d) return set_error(kInvalid, "dhidden leading dimension < d");
   if (dweight && ld_dweight < d) return set_error(kInvalid, "dweight leading dimension < d");
   if (reinterpret_cast<unsigned long>(workspace) % 256) return set_error(kInvalid, "workspace must be 256-byte aligned");
+  if (int rc = check_out_stride(vocab, 2, "logit-gradient chunk")) return rc;
+  if (int rc = check_out_stride(ld_dhidden, 2, "dhidden")) return rc;
+  if (int rc = check_out_stride(d, 4, "dhidden partial")) return rc;
+  if (dweight) {
+    if (int rc = check_out_stride(ld_dweight, 4, "dweight")) return rc;
+  }
   hipStream_t s = static_cast<hipStream_t>(stream);
   const long chunk = chunk_rows < rows ? chunk_rows : rows;
   const int splits = ce_dh_splits(chunk, d, vocab);

@@ -47,6 +47,7 @@ extern "C" int ws_rmsnorm_gate_mm(const void* x, int64_t x_s0, const float* norm
     return set_error(kInvalid, "gate column range [%ld, %ld) outside [0, %ld)", (long)gate_begin,
                      (long)gate_end, (long)n);
   if (x_s0 < k) return set_error(kInvalid, "RMSNorm prologue needs row-contiguous x");
+  if (int rc = check_out_stride(n, 2, "output")) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
   // Prologue: one pass over x writes the normalized BF16 operand y and rstd.
   const int vec = (x_s0 % 8 == 0) && (k % 8 == 0) && al(x, 16) && al(normed, 16);
@@ -76,6 +77,8 @@ extern "C" int ws_residual_mm(const void* a, int64_t a_s0, int64_t a_s1, const v
                               void* stream) {
   if (int rc = check_gemm_args(a, a_s0, a_s1, b, b_s0, b_s1, out, m, n, k)) return rc;
   if (!residual || ld_residual < n) return set_error(kInvalid, "invalid residual operand");
+  if (int rc = check_out_stride(n, 2, "output")) return rc;
+  if (int rc = check_out_stride(ld_residual, 2, "residual")) return rc;
   GemmParams p{};
   p.a = desc_a(a, a_s0, a_s1);
   p.b = desc_b(b, b_s0, b_s1);
@@ -100,6 +103,7 @@ extern "C" int ws_swiglu_backward_mm(const void* grad, int64_t g_s0, int64_t g_s
                                      int eager_rounding, void* stream) {
   if (int rc = check_gemm_args(grad, g_s0, g_s1, b, b_s0, b_s1, dpacked, m, h, k)) return rc;
   if (!packed) return set_error(kInvalid, "null packed projection");
+  if (int rc = check_out_stride(2 * h, 2, "packed projection")) return rc;
   GemmParams p{};
   p.a = desc_a(grad, g_s0, g_s1);
   p.b = desc_b(b, b_s0, b_s1);
@@ -198,6 +202,7 @@ extern "C" int ws_mm_accumulate_f32(const void* a, int64_t a_s0, int64_t a_s1, c
   if (ldg < n) return set_error(kInvalid, "gradient leading dimension %ld < n", (long)ldg);
   if (splits < 1 || splits > 64) return set_error(kInvalid, "splits must be in [1, 64]");
   if (splits > 1 && !workspace) return set_error(kInvalid, "split-K needs a workspace");
+  if (int rc = check_out_stride(ldg, 4, "gradient")) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
   GemmParams p{};
   p.a = desc_a(a, a_s0, a_s1);

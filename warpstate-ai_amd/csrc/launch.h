@@ -112,6 +112,17 @@ int dispatch(const GemmParams& p, int am, int bm, LaunchCfg cfg, hipStream_t s) 
 
 inline bool fits_i32(long v) { return v >= 0 && v < 0x7fffffffL; }
 
+// Epilogues address an output tile through a buffer resource of at most 2 GiB that starts
+// at the tile's first row, so 256 rows of an output (row stride `ld` elements of
+// `elem_bytes`) must span less than that; wider outputs are rejected instead of losing
+// stores past the limit.
+inline int check_out_stride(long ld, int elem_bytes, const char* what) {
+  if ((long)kFBM * ld * elem_bytes + (long)kFBN * elem_bytes >= 0x7fffffffL)
+    return set_error(kInvalid, "%s row stride %ld is too large: a 256-row tile spans 2 GiB or more",
+                     what, ld);
+  return kOk;
+}
+
 // Fast path (gemm_fast.h): 256 x 256 tiles, direct-to-LDS loads, 16x16x32 MFMA.
 template <int AM, int BMD, bool PAIRED, class Epi>
 int run_fast(GemmParams p, LaunchCfg cfg, hipStream_t stream) {

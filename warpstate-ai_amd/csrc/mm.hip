@@ -39,6 +39,7 @@ extern "C" int ws_mm(const void* a, int64_t a_s0, int64_t a_s1, const void* b, i
   if (int rc = check_gemm_args(a, a_s0, a_s1, b, b_s0, b_s1, c, m, n, k)) return rc;
   if (algorithm < 0 || algorithm > 2) return set_error(kInvalid, "unknown algorithm %d", algorithm);
   if (tile != kTileLarge && tile != kTileSmall) return set_error(kInvalid, "unknown tile %d", tile);
+  if (int rc = check_out_stride(n, 2, "output")) return rc;
   GemmParams p{};
   p.a = desc_a(a, a_s0, a_s1);
   p.b = desc_b(b, b_s0, b_s1);
@@ -65,6 +66,7 @@ extern "C" int ws_swiglu_mm(const void* a, int64_t a_s0, int64_t a_s1, const voi
   if (!act) return set_error(kInvalid, "null activation pointer");
   if (algorithm < 0 || algorithm > 1) return set_error(kInvalid, "unknown SwiGLU algorithm %d", algorithm);
   if (tile != kTileLarge && tile != kTileSmall) return set_error(kInvalid, "unknown tile %d", tile);
+  if (int rc = check_out_stride(2 * h, 2, "packed output")) return rc;
   GemmParams p{};
   p.a = desc_a(a, a_s0, a_s1);
   p.b = desc_b(b, b_s0, b_s1);
