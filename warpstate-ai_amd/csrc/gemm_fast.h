@@ -575,129 +575,9 @@ __global__ void __launch_bounds__(kFNT) gemm_fast_kernel(const GemmParams p) {
     else b_rb[j] = wn * TN + 16 * j;
   }
 
-  if constexpr (std::is_same<Epi, FEpiAccF32<false>>::value) {
-    // Balanced accumulation (the other instantiations keep the plain tile loop).
-    // One output tile (raster index t) over k-tiles [kb, ke), then `epi(acc, m_base, n_base,
-    // tm, tn)` and a barrier (the next tile's loads reuse the epilogue's staging space).
-    auto run_tile = [&](int t, int kb, int ke, auto&& epi) {
-      int tm, tn;
-      tile_position(t, p.tiles_m, p.tiles_n, tm, tn);
-      const int row0_a = tm * kFBM;
-      const int row0_b = tn * bn_cols;
-      la.init(p.a, row0_a, p.M, 0, wave, lane);
-      lb.init(p.b, row0_b, PAIRED ? p.H : p.N, PAIRED ? p.H : 0, wave, lane);
-
-      Acc16<FA, FB> acc;
-#pragma unroll
-      for (int i = 0; i < FA; ++i)
-#pragma unroll
-        for (int j = 0; j < FB; ++j) acc.v[i][j] = f32x4_v{0.f, 0.f, 0.f, 0.f};
-
-      if (kb < ke) {
-        la.issue(p.a, row0_a, kb * kFBK, p.K, fsmem, wave, lane);
-        lb.issue(p.b, row0_b, kb * kFBK, p.K, fsmem + kFTileBytes, wave, lane);
-        for (int kt = kb; kt < ke; ++kt) {
-          const int cur = (kt - kb) & 1;
-          __builtin_amdgcn_s_waitcnt(wait_vmcnt(0));
-          __builtin_amdgcn_s_barrier();
-          if (!kMidIssue && kt + 1 < ke) {
-            unsigned char* nxt = fsmem + (cur ^ 1) * kFStageBytes;
-            la.issue(p.a, row0_a, (kt + 1) * kFBK, p.K, nxt, wave, lane);
-            lb.issue(p.b, row0_b, (kt + 1) * kFBK, p.K, nxt + kFTileBytes, wave, lane);
-          }
-          const unsigned char* sa = fsmem + cur * kFStageBytes;
-          const unsigned char* sb = sa + kFTileBytes;
-          bf16x8_t af[2][FA], bfr[2][FB];
-#pragma unroll
-          for (int i = 0; i < FA; ++i) af[0][i] = read_frag<AMODE>(sa, wm * TM + 16 * i, 0, lane);
-#pragma unroll
-          for (int j = 0; j < FB; ++j) bfr[0][j] = read_frag<BMODE>(sb, b_rb[j], 0, lane);
-#pragma unroll
-          for (int s = 0; s < kFBK / 32; ++s) {
-            if (kMidIssue && s == 1) {
-              // Step-0 reads first, then step 1's reads spread over step 0's MFMAs; then the
-              // next k-tile's loads, after this wave's last fragment read of the tile.
-              __builtin_amdgcn_sched_group_barrier(0x100, NR, 0);
-#pragma unroll
-              for (int r = 0; r < NR; ++r) {
-                __builtin_amdgcn_sched_group_barrier(0x008, NM / NR > 0 ? NM / NR : 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-              }
-              __builtin_amdgcn_sched_group_barrier(0x008, NM - (NM / NR > 0 ? NM / NR : 1) * NR, 0);
-              __builtin_amdgcn_sched_barrier(0);
-              if (kt + 1 < ke) {
-                unsigned char* nxt = fsmem + (cur ^ 1) * kFStageBytes;
-                la.issue(p.a, row0_a, (kt + 1) * kFBK, p.K, nxt, wave, lane);
-                lb.issue(p.b, row0_b, (kt + 1) * kFBK, p.K, nxt + kFTileBytes, wave, lane);
-              }
-              __builtin_amdgcn_sched_barrier(0);
-            }
-            if (s + 1 < kFBK / 32) {
-#pragma unroll
-              for (int i = 0; i < FA; ++i) af[(s + 1) & 1][i] = read_frag<AMODE>(sa, wm * TM + 16 * i, s + 1, lane);
-#pragma unroll
-              for (int j = 0; j < FB; ++j) bfr[(s + 1) & 1][j] = read_frag<BMODE>(sb, b_rb[j], s + 1, lane);
-            }
-#pragma unroll
-            for (int i = 0; i < FA; ++i)
-#pragma unroll
-              for (int j = 0; j < FB; ++j)
-                acc.v[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bfr[s & 1][j], af[s & 1][i],
-                                                                       acc.v[i][j], 0, 0, 0);
-          }
-          if constexpr (kMidIssue) {
-            __builtin_amdgcn_sched_group_barrier(0x008, NM, 0);
-          } else {
-            // Step-0 reads first, then step 1's reads spread over step 0's MFMAs.
-            __builtin_amdgcn_sched_group_barrier(0x100, NR, 0);
-#pragma unroll
-            for (int r = 0; r < NR; ++r) {
-              __builtin_amdgcn_sched_group_barrier(0x008, NM / NR > 0 ? NM / NR : 1, 0);
-              __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-            }
-            __builtin_amdgcn_sched_group_barrier(0x008, NM - (NM / NR > 0 ? NM / NR : 1) * NR, 0);
-            __builtin_amdgcn_sched_group_barrier(0x008, NM, 0);
-          }
-        }
-        // All waves are done reading both stages before the next tile's first load.
-        __builtin_amdgcn_s_barrier();
-      }
-      const int m_base = row0_a + wm * TM;
-      const int n_base = row0_b + (PAIRED ? wn * (TN / 2) : wn * TN);
-      epi(acc, m_base, n_base, tm, tn);
-      __builtin_amdgcn_s_barrier();
-    };
-    if (p.balanced) {
-      // Whole tiles, accumulated straight into G.
-      for (int w = blockIdx.x; w < p.dp_tiles; w += gridDim.x)
-        run_tile(xcd_remap(w, p.dp_tiles, gridDim.x), 0, p.k_tiles,
-                 [&](auto& acc, int m_base, int n_base, int tm, int tn) {
-                   Epi::run(p, acc, m_base, n_base, lane, tm, tn, wn, fsmem + wave * kFStageWave);
-                 });
-      // This workgroup's stream-K share of the remaining tiles' k-tiles. Worker indices
-      // run XCD-contiguous (the dispatcher deals workgroups round-robin to the XCDs) so
-      // that the pieces running together on one XCD belong to neighbouring tiles.
-      const long W = gridDim.x, b = blockIdx.x;
-      const long v = W % kXcds == 0 ? (b % kXcds) * (W / kXcds) + b / kXcds : b;
-      long x = sk_begin(v, p.sk_units, W);
-      const long end = sk_begin(v + 1, p.sk_units, W);
-      while (x < end) {
-        const long ti = x / p.k_tiles;
-        const int kb = (int)(x - ti * p.k_tiles);
-        const int ke = (int)min((long)p.k_tiles, kb + (end - x));
-        const long piece = v - sk_worker(ti * p.k_tiles, p.sk_units, W);
-        float* block = p.sk_ws + (ti * p.sk_pieces + piece) * (long)(kFBM * kFBN);
-        run_tile(p.dp_tiles + (int)ti, kb, ke,
-                 [&](auto& acc, int m_base, int n_base, int tm, int tn) {
-                   FEpiPartial::run(acc, m_base - tm * kFBM, n_base - tn * kFBN, lane, block);
-                 });
-        x += ke - kb;
-      }
-      return;
-    }
-  }
-  for (int w = blockIdx.x; w < p.total_tiles; w += gridDim.x) {
-    const int t = xcd_remap(w, p.total_tiles, gridDim.x);
+  // One output tile (raster index t) over k-tiles [kb, ke), then `epi(acc, m_base, n_base,
+  // tm, tn)` and a barrier (the next tile's loads reuse the epilogue's staging space).
+  auto run_tile = [&](int t, int kb, int ke, auto&& epi) {
     int tm, tn;
     tile_position(t, p.tiles_m, p.tiles_n, tm, tn);
     const int row0_a = tm * kFBM;
@@ -711,14 +591,14 @@ __global__ void __launch_bounds__(kFNT) gemm_fast_kernel(const GemmParams p) {
 #pragma unroll
       for (int j = 0; j < FB; ++j) acc.v[i][j] = f32x4_v{0.f, 0.f, 0.f, 0.f};
 
-    if (kt_begin < kt_end) {
-      la.issue(p.a, row0_a, kt_begin * kFBK, p.K, fsmem, wave, lane);
-      lb.issue(p.b, row0_b, kt_begin * kFBK, p.K, fsmem + kFTileBytes, wave, lane);
-      for (int kt = kt_begin; kt < kt_end; ++kt) {
-        const int cur = (kt - kt_begin) & 1;
+    if (kb < ke) {
+      la.issue(p.a, row0_a, kb * kFBK, p.K, fsmem, wave, lane);
+      lb.issue(p.b, row0_b, kb * kFBK, p.K, fsmem + kFTileBytes, wave, lane);
+      for (int kt = kb; kt < ke; ++kt) {
+        const int cur = (kt - kb) & 1;
         __builtin_amdgcn_s_waitcnt(wait_vmcnt(0));
         __builtin_amdgcn_s_barrier();
-        if (!kMidIssue && kt + 1 < kt_end) {
+        if (!kMidIssue && kt + 1 < ke) {
           unsigned char* nxt = fsmem + (cur ^ 1) * kFStageBytes;
           la.issue(p.a, row0_a, (kt + 1) * kFBK, p.K, nxt, wave, lane);
           lb.issue(p.b, row0_b, (kt + 1) * kFBK, p.K, nxt + kFTileBytes, wave, lane);
@@ -743,7 +623,7 @@ __global__ void __launch_bounds__(kFNT) gemm_fast_kernel(const GemmParams p) {
             }
             __builtin_amdgcn_sched_group_barrier(0x008, NM - (NM / NR > 0 ? NM / NR : 1) * NR, 0);
             __builtin_amdgcn_sched_barrier(0);
-            if (kt + 1 < kt_end) {
+            if (kt + 1 < ke) {
               unsigned char* nxt = fsmem + (cur ^ 1) * kFStageBytes;
               la.issue(p.a, row0_a, (kt + 1) * kFBK, p.K, nxt, wave, lane);
               lb.issue(p.b, row0_b, (kt + 1) * kFBK, p.K, nxt + kFTileBytes, wave, lane);
@@ -782,10 +662,45 @@ __global__ void __launch_bounds__(kFNT) gemm_fast_kernel(const GemmParams p) {
     }
     const int m_base = row0_a + wm * TM;
     const int n_base = row0_b + (PAIRED ? wn * (TN / 2) : wn * TN);
-    Epi::run(p, acc, m_base, n_base, lane, tm, tn, wn, fsmem + wave * kFStageWave);
-    // The next tile's loads reuse the staging space.
+    epi(acc, m_base, n_base, tm, tn);
     __builtin_amdgcn_s_barrier();
+  };
+  if constexpr (std::is_same<Epi, FEpiAccF32<false>>::value) {
+    // Balanced accumulation (the other instantiations use the plain tile loop below).
+    if (p.balanced) {
+      // Whole tiles, accumulated straight into G.
+      for (int w = blockIdx.x; w < p.dp_tiles; w += gridDim.x)
+        run_tile(xcd_remap(w, p.dp_tiles, gridDim.x), 0, p.k_tiles,
+                 [&](auto& acc, int m_base, int n_base, int tm, int tn) {
+                   Epi::run(p, acc, m_base, n_base, lane, tm, tn, wn, fsmem + wave * kFStageWave);
+                 });
+      // This workgroup's stream-K share of the remaining tiles' k-tiles. Worker indices
+      // run XCD-contiguous (the dispatcher deals workgroups round-robin to the XCDs) so
+      // that the pieces running together on one XCD belong to neighbouring tiles.
+      const long W = gridDim.x, b = blockIdx.x;
+      const long v = W % kXcds == 0 ? (b % kXcds) * (W / kXcds) + b / kXcds : b;
+      long x = sk_begin(v, p.sk_units, W);
+      const long end = sk_begin(v + 1, p.sk_units, W);
+      while (x < end) {
+        const long ti = x / p.k_tiles;
+        const int kb = (int)(x - ti * p.k_tiles);
+        const int ke = (int)min((long)p.k_tiles, kb + (end - x));
+        const long piece = v - sk_worker(ti * p.k_tiles, p.sk_units, W);
+        float* block = p.sk_ws + (ti * p.sk_pieces + piece) * (long)(kFBM * kFBN);
+        run_tile(p.dp_tiles + (int)ti, kb, ke,
+                 [&](auto& acc, int m_base, int n_base, int tm, int tn) {
+                   FEpiPartial::run(acc, m_base - tm * kFBM, n_base - tn * kFBN, lane, block);
+                 });
+        x += ke - kb;
+      }
+      return;
+    }
   }
+  for (int w = blockIdx.x; w < p.total_tiles; w += gridDim.x)
+    run_tile(xcd_remap(w, p.total_tiles, gridDim.x), kt_begin, kt_end,
+             [&](auto& acc, int m_base, int n_base, int tm, int tn) {
+               Epi::run(p, acc, m_base, n_base, lane, tm, tn, wn, fsmem + wave * kFStageWave);
+             });
 }
 
 }  // namespace ws
