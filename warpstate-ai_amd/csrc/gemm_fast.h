@@ -52,6 +52,12 @@ constexpr int kFStageRow = 272;
 constexpr int kFStageWave = 64 * kFStageRow;
 constexpr int kFLdsAlloc = 8 * kFStageWave > kFLdsBytes ? 8 * kFStageWave : kFLdsBytes;
 constexpr int kFIns = kFTileBytes / (kFNT * 16);         // 4 loads per thread per operand
+// Cache policy of the epilogues' outputs and auxiliary inputs: non-temporal. Each is
+// touched once, in bursts when all CUs reach their epilogues together, and it should not
+// displace the operand tiles that other workgroups are still reading from L2 (dAct 4-5 %
+// faster). The FP32 accumulation keeps the default: its gradient and split-K partial
+// blocks are read again soon.
+constexpr int kEpiNT = 2;
 
 typedef float f32x4_v __attribute__((ext_vector_type(4)));
 typedef short i16x4_t __attribute__((ext_vector_type(4)));
@@ -212,10 +218,10 @@ struct FEpiStore {
         const bool ok = m_base + r < p.M;
         const long off = (long)r * p.ldaux + c8;
         if (full) {
-          rv[q] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rr, store_off(ok, off, 2), 0, 0));
+          rv[q] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rr, store_off(ok, off, 2), 0, kEpiNT));
         } else {
           const u32x2_t h = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(
-              rr, store_off(ok && half, off, 2), 0, 0));
+              rr, store_off(ok && half, off, 2), 0, kEpiNT));
           rv[q] = u32x4_t{h[0], h[1], 0u, 0u};
         }
       }
@@ -232,10 +238,10 @@ struct FEpiStore {
       }
       const long off = (long)r * p.ldc + c8;
       if (full) {
-        __builtin_amdgcn_raw_buffer_store_b128(vd, rc, store_off(ok, off, 2), 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b128(vd, rc, store_off(ok, off, 2), 0, kEpiNT);
       } else {
         const u32x2_t h = {vd[0], vd[1]};
-        __builtin_amdgcn_raw_buffer_store_b64(h, rc, store_off(ok && half, off, 2), 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b64(h, rc, store_off(ok && half, off, 2), 0, kEpiNT);
       }
     }
   }
@@ -285,14 +291,14 @@ struct FEpiSwiglu {
       }
       const long po = (long)r * p.ldc + c8, ao = (long)r * p.ldc2 + c8;
       if (full) {
-        __builtin_amdgcn_raw_buffer_store_b128(vu, rp, store_off(ok, po, 2), 0, 0);
-        __builtin_amdgcn_raw_buffer_store_b128(vg, rp, store_off(ok, po + hoff, 2), 0, 0);
-        __builtin_amdgcn_raw_buffer_store_b128(va, ra, store_off(ok, ao, 2), 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b128(vu, rp, store_off(ok, po, 2), 0, kEpiNT);
+        __builtin_amdgcn_raw_buffer_store_b128(vg, rp, store_off(ok, po + hoff, 2), 0, kEpiNT);
+        __builtin_amdgcn_raw_buffer_store_b128(va, ra, store_off(ok, ao, 2), 0, kEpiNT);
       } else {
         const bool okh = ok && half;
-        __builtin_amdgcn_raw_buffer_store_b64(u32x2_t{vu[0], vu[1]}, rp, store_off(okh, po, 2), 0, 0);
-        __builtin_amdgcn_raw_buffer_store_b64(u32x2_t{vg[0], vg[1]}, rp, store_off(okh, po + hoff, 2), 0, 0);
-        __builtin_amdgcn_raw_buffer_store_b64(u32x2_t{va[0], va[1]}, ra, store_off(okh, ao, 2), 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b64(u32x2_t{vu[0], vu[1]}, rp, store_off(okh, po, 2), 0, kEpiNT);
+        __builtin_amdgcn_raw_buffer_store_b64(u32x2_t{vg[0], vg[1]}, rp, store_off(okh, po + hoff, 2), 0, kEpiNT);
+        __builtin_amdgcn_raw_buffer_store_b64(u32x2_t{va[0], va[1]}, ra, store_off(okh, ao, 2), 0, kEpiNT);
       }
     }
   }
@@ -351,8 +357,8 @@ struct FEpiSwigluBwd {
           const int m = m_base + r;
           const bool ok = m < p.M && n + 7 < p.N;
           const long off = (long)r * p.ldaux + c8;
-          vu[q][h] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rp, store_off(ok, off, 2), 0, 0));
-          vg[q][h] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rp, store_off(ok, off + hoff, 2), 0, 0));
+          vu[q][h] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rp, store_off(ok, off, 2), 0, kEpiNT));
+          vg[q][h] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rp, store_off(ok, off + hoff, 2), 0, kEpiNT));
         }
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
@@ -372,8 +378,8 @@ struct FEpiSwigluBwd {
             og[d] = pack_bf16x2(dg0, dg1);
           }
           const long off = (long)r * p.ldc + c8;
-          __builtin_amdgcn_raw_buffer_store_b128(od, rd, store_off(ok, off, 2), 0, 0);
-          __builtin_amdgcn_raw_buffer_store_b128(og, rd, store_off(ok, off + hoff, 2), 0, 0);
+          __builtin_amdgcn_raw_buffer_store_b128(od, rd, store_off(ok, off, 2), 0, kEpiNT);
+          __builtin_amdgcn_raw_buffer_store_b128(og, rd, store_off(ok, off + hoff, 2), 0, kEpiNT);
         }
       }
     }
@@ -528,9 +534,9 @@ struct FEpiCEGrad {
       }
       const long off = (long)r * p.ldc + c8;
       if (full) {
-        __builtin_amdgcn_raw_buffer_store_b128(o, rc, store_off(ok, off, 2), 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b128(o, rc, store_off(ok, off, 2), 0, kEpiNT);
       } else {
-        __builtin_amdgcn_raw_buffer_store_b64(u32x2_t{o[0], o[1]}, rc, store_off(ok && half, off, 2), 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b64(u32x2_t{o[0], o[1]}, rc, store_off(ok && half, off, 2), 0, kEpiNT);
       }
     }
   }
