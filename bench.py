@@ -125,8 +125,8 @@ def run_step(inp, out, timer=None):
     from contextlib import nullcontext
 
     from ops.activation_execution import _rms_backward
-    from ops.fused_execution import (mm, mm_accumulate_, residual_mm, rmsnorm_gate_mm,
-                                     sigmoid_backward_cols, swiglu_backward_mm)
+    from ops.fused_execution import (mm, mm_accumulate_, mm_accumulate_group_, residual_mm,
+                                     rmsnorm_gate_mm, sigmoid_backward_cols, swiglu_backward_mm)
     from ops.matmul_epilogue import launch_swiglu_mm
 
     reg = timer.region if timer else (lambda name: nullcontext())
@@ -144,10 +144,10 @@ def run_step(inp, out, timer=None):
                                          out=out["dpacked"])
         with reg("mlp_bwd.dx"):
             mm(dpacked, inp["mlp_w_upgate"])
-        with reg("mlp_bwd.wgrad_down"):
-            mm_accumulate_(inp["mlp_g_down"], inp["mlp_dy"].T, act, True)
-        with reg("mlp_bwd.wgrad_upgate"):
-            mm_accumulate_(inp["mlp_g_upgate"], dpacked.T, inp["mlp_x"], True)
+        with reg("mlp_bwd.wgrad"):
+            # W_down's and W_upgate's gradients in one launch (both reduce over tokens).
+            mm_accumulate_group_([(inp["mlp_g_down"], inp["mlp_dy"].T, act),
+                                  (inp["mlp_g_upgate"], dpacked.T, inp["mlp_x"])], True)
     with reg("qkv_bwd"):
         # Backward of RMSNorm -> projection -> gate sigmoid (rmsnorm_gate_mm_backward with
         # in_place=True): the incoming gradient of the projection output has no other
@@ -191,7 +191,7 @@ def bench_gpu(args):
         regions[name] = {"ms": round(ms, 4), "tflops": round(f / ms / 1e9, 1),
                          "pct_peak": round(100 * f / ms / 1e9 / PEAK_BF16_TFLOPS, 2)}
     sub = {"mlp_bwd.dact_swiglu": 2 * m * D * FFN, "mlp_bwd.dx": 2 * m * 2 * FFN * D,
-           "mlp_bwd.wgrad_down": 2 * D * FFN * m, "mlp_bwd.wgrad_upgate": 2 * 2 * FFN * D * m,
+           "mlp_bwd.wgrad": 2 * D * FFN * m + 2 * 2 * FFN * D * m,
            "qkv_bwd.dx": 2 * m * NQKV * D, "qkv_bwd.wgrad": 2 * NQKV * m * D}
     kernels = {}
     for name, f in sub.items():

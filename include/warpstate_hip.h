@@ -6,7 +6,8 @@
  * torch.cuda.current_stream().cuda_stream of the calling thread). The library launches
  * work on that stream and returns; it never allocates, frees or synchronises. The caller
  * allocates every output and workspace. Outputs must not alias inputs, except the FP32
- * gradient buffer of ws_mm_accumulate_f32 (updated in place) and the output of
+ * gradient buffers of ws_mm_accumulate_f32 and ws_mm_accumulate_f32_group (updated in
+ * place) and the output of
  * ws_sigmoid_backward_cols (which may be its dout).
  *
  * Return value: 0 on success, 1 for an invalid argument (nothing was launched), 2 for a
@@ -156,6 +157,37 @@ int64_t ws_mm_accumulate_workspace_floats(int64_t m, int64_t n, int64_t k, int64
 int ws_mm_accumulate_f32(const void* a, int64_t a_s0, int64_t a_s1, const void* b, int64_t b_s0,
                          int64_t b_s1, float* g, int64_t ldg, int64_t m, int64_t n, int64_t k,
                          int round_bf16, float* workspace, int64_t splits, void* stream);
+
+/* One weight gradient of a grouped accumulation: G[m, n] (row stride ldg) += A[m, k] B[k, n],
+ * with A and B given by pointer and (row, column) element strides as in ws_mm. */
+typedef struct ws_accumulate_problem {
+  const void* a;
+  int64_t a_s0, a_s1;
+  const void* b;
+  int64_t b_s0, b_s1;
+  float* g;
+  int64_t ldg;
+  int64_t m, n;
+} ws_accumulate_problem;
+
+/* Floats of the workspace ws_mm_accumulate_f32_group needs for these problems (0 when
+ * none), on the current device. */
+int64_t ws_mm_accumulate_group_workspace_floats(const ws_accumulate_problem* problems, int count,
+                                                int64_t k);
+
+/*
+ * Up to four weight-gradient accumulations with the same reduction length k (the token
+ * count) in one launch, each with the numerics of ws_mm_accumulate_f32 (round_bf16 as
+ * there): the weight gradients of one backward stage, computed together instead of as
+ * separate AccumulateGrad steps (ops/matmul_execution.py:243 once per weight; fused, new).
+ * Their 256 x 256 tiles form one raster: whole rounds of the GPU run directly, the rest
+ * is shared evenly by all compute units through `workspace`, so a gradient with fewer
+ * tiles than compute units fills the GPU together with the others. The gradients must not
+ * overlap. When the problems' operand layouts differ or do not take the fast loader, the
+ * call runs ws_mm_accumulate_f32 per problem (split-K through `workspace` when given).
+ */
+int ws_mm_accumulate_f32_group(const ws_accumulate_problem* problems, int count, int64_t k,
+                               int round_bf16, float* workspace, void* stream);
 
 /* Number of per-row partials (floats per row of part_max / part_sum) for `vocab`. */
 int64_t ws_linear_ce_parts(int64_t vocab);

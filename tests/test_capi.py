@@ -72,3 +72,45 @@ def test_invalid_arguments_are_rejected_before_any_launch():
     with pytest.raises(RuntimeError, match="row stride"):
         _hip.call("ws_mm_accumulate_f32", 16, 8, 1, 16, 8, 1, 16, 2_100_000, 16, 8, 8, 1, None,
                   1, None)
+
+
+def test_grouped_accumulation_arguments_are_rejected_before_any_launch():
+    """Group size, per-gradient shapes and overlapping gradients are checked on the host."""
+    gpu_ptr = 1 << 20  # never dereferenced: every call below fails validation first
+
+    def row(g, m, n, ldg=None):
+        return (gpu_ptr, 8, 1, gpu_ptr, 8, 1, g, ldg or n, m, n)
+
+    table = _hip.problem_table([row(gpu_ptr, 8, 8)] * 5)
+    with pytest.raises(RuntimeError, match="group size 5"):
+        _hip.call("ws_mm_accumulate_f32_group", table, 5, 8, 1, None, None)
+    with pytest.raises(RuntimeError, match="group size 0"):
+        _hip.call("ws_mm_accumulate_f32_group", table, 0, 8, 1, None, None)
+    with pytest.raises(RuntimeError, match="null problem table"):
+        _hip.call("ws_mm_accumulate_f32_group", None, 1, 8, 1, None, None)
+    with pytest.raises(RuntimeError, match="positive"):
+        _hip.call("ws_mm_accumulate_f32_group", _hip.problem_table([row(gpu_ptr, 0, 8)]), 1, 8,
+                  1, None, None)
+    with pytest.raises(RuntimeError, match="row stride"):
+        _hip.call("ws_mm_accumulate_f32_group",
+                  _hip.problem_table([row(gpu_ptr, 8, 8, 2_100_000)]), 1, 8, 1, None, None)
+    # The second gradient starts inside the first one's last row.
+    overlapping = _hip.problem_table([row(gpu_ptr, 8, 8), row(gpu_ptr + 4 * (7 * 8 + 4), 8, 8)])
+    with pytest.raises(RuntimeError, match="overlap"):
+        _hip.call("ws_mm_accumulate_f32_group", overlapping, 2, 8, 1, None, None)
+
+
+def test_grouped_workspace_query():
+    """Whole rounds need no workspace; the shared tiles need one 256 x 256 FP32 block per
+    piece; a group that falls back needs what its largest single split needs."""
+    def rows(*shapes):
+        return _hip.problem_table([(1 << 20, 8, 1, 1 << 20, 8, 1, 1 << 20, n, m, n)
+                                   for m, n in shapes])
+
+    q = lambda t, c, k: _hip.query("ws_mm_accumulate_group_workspace_floats", t, c, k)
+    assert q(None, 1, 64) == 0
+    # 2048 x 2048 twice at k = 16384: 128 tiles, no whole round; each falls back to 2
+    # even splits (256 tiles), which need 2 x 2048 x 2048 floats.
+    assert q(rows((2048, 2048), (2048, 2048)), 2, 16384) >= 2 * 2048 * 2048
+    need = q(rows((2048, 5632), (11264, 2048)), 2, 16384)
+    assert need > 0 and need % 65536 == 0

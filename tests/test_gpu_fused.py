@@ -214,14 +214,17 @@ def test_balanced_accumulation_whole_rounds_plus_shared_tiles():
     assert_f32_close(balanced.cpu(), plain.cpu(), "balanced vs unsplit")
 
 
-@pytest.mark.parametrize("round_bf16", [True, False])
-def test_balanced_accumulation_ragged_tiles(round_bf16):
+@pytest.mark.parametrize("round_bf16,tokens", [(True, 1000), (False, 1000), (True, 520)])
+def test_balanced_accumulation_ragged_tiles(round_bf16, tokens):
     """The balanced split with ragged rows, columns and k: 17 x 16 tiles whose last row
-    and column of tiles are partial, 1000-long reduction (the last k-tile partial)."""
+    and column of tiles are partial, 1000-long reduction (the last k-tile partial). Both
+    widths are multiples of 8, so the M/N-contiguous operands take the fast loader and the
+    balanced plan (other widths take the generic loader and even slices). With 520 tokens
+    the 16 shared tiles hold 16 x 9 = 144 k-tiles, fewer than the 256 workgroups."""
     from ops.fused_execution import mm_accumulate_
 
     gen = _gen(79)
-    tokens, n_out, n_in = 1000, 17 * 256 - 100, 16 * 256 - 36
+    n_out, n_in = 17 * 256 - 96, 16 * 256 - 40
     dy = torch.randn(tokens, n_out, generator=gen).bfloat16()
     x = torch.randn(tokens, n_in, generator=gen).bfloat16()
     g = torch.randn(n_out, n_in, generator=gen) * 1e-2
@@ -248,6 +251,73 @@ def test_balanced_accumulation_ragged_edges(round_bf16):
     torch.cuda.synchronize()
     assert_f32_close(gg.cpu(), oracle.accumulate_weight_grad(g, dy.T, x, round_bf16),
                      f"ragged round={round_bf16}")
+
+
+def _group_case(seed, tokens, shapes, mn_layout=True):
+    """(G, a, b) triples on the GPU: a = dY^T, b = X with `tokens` rows (the weight-gradient
+    layout, both operands M/N-contiguous) or, with mn_layout False, a K-contiguous a."""
+    gen = _gen(seed)
+    cases = []
+    for n_out, n_in in shapes:
+        dy = torch.randn(tokens, n_out, generator=gen).bfloat16()
+        x = torch.randn(tokens, n_in, generator=gen).bfloat16()
+        g = torch.randn(n_out, n_in, generator=gen) * 1e-2
+        a = dy.cuda().T if mn_layout else dy.T.contiguous().cuda()
+        cases.append((g, dy.T, x, g.cuda(), a, x.cuda()))
+    return cases
+
+
+@pytest.mark.parametrize("round_bf16", [True, False])
+def test_grouped_accumulation_shares_tiles_across_gradients(round_bf16):
+    """Three gradients in one launch: 128 + 144 + 4 = 276 tiles on 256 CUs, so the first
+    256 run whole and the last 20 (16 of the second gradient, all 4 of the third) share
+    the k-range; ragged rows, columns and k (520 tokens: the last k-tile partial). Widths
+    are multiples of 8 (fast loader, one launch). The whole tiles match the unsplit call
+    bit for bit: the same tile computation, only scheduled differently."""
+    from ops.fused_execution import mm_accumulate_, mm_accumulate_group_
+
+    cases = _group_case(81, 520, [(2000, 4000), (4000, 2104), (296, 296)])
+    plain = [gg.clone() for _, _, _, gg, _, _ in cases]
+    for (_, _, _, _, ga, gb), gp in zip(cases, plain):
+        mm_accumulate_(gp, ga, gb, round_bf16, 1)
+    mm_accumulate_group_([(gg, ga, gb) for _, _, _, gg, ga, gb in cases], round_bf16)
+    torch.cuda.synchronize()
+    for i, (g, a, b, gg, _, _) in enumerate(cases):
+        assert_f32_close(gg.cpu(), oracle.accumulate_weight_grad(g, a, b, round_bf16),
+                         f"gradient {i} round={round_bf16}")
+    assert torch.equal(cases[0][3], plain[0])  # all 128 tiles of the first run whole
+
+
+def test_grouped_accumulation_of_one_matches_the_balanced_call_bitwise():
+    """A group of one runs the same balanced plan as ws_mm_accumulate_f32 with splits > 1."""
+    from ops.fused_execution import mm_accumulate_, mm_accumulate_group_
+
+    (g, a, b, gg, ga, gb), = _group_case(82, 1024, [(17 * 256 - 96, 16 * 256 - 40)])
+    single = gg.clone()
+    mm_accumulate_group_([(gg, ga, gb)], True)
+    mm_accumulate_(single, ga, gb, True, 2)
+    torch.cuda.synchronize()
+    assert torch.equal(gg, single)
+    rows = torch.cat([torch.arange(0, 32), torch.arange(g.shape[0] - 200, g.shape[0])])
+    assert_f32_close(gg.cpu()[rows], oracle.accumulate_weight_grad(g[rows], a[rows], b),
+                     "group of one, sampled rows")
+
+
+@pytest.mark.parametrize("case", ["few_tiles", "mixed_layouts"])
+def test_grouped_accumulation_falls_back_to_single_launches(case):
+    """Fewer tiles than CUs, or operand layouts that differ between the gradients: each
+    gradient then takes ws_mm_accumulate_f32 with its own split."""
+    from ops.fused_execution import mm_accumulate_group_
+
+    if case == "few_tiles":
+        cases = _group_case(83, 3000, [(300, 264), (520, 130)])
+    else:
+        cases = (_group_case(84, 1024, [(4096, 4096)]) +
+                 _group_case(85, 1024, [(1024, 2048)], mn_layout=False))
+    mm_accumulate_group_([(gg, ga, gb) for _, _, _, gg, ga, gb in cases], True)
+    torch.cuda.synchronize()
+    for i, (g, a, b, gg, _, _) in enumerate(cases):
+        assert_f32_close(gg.cpu(), oracle.accumulate_weight_grad(g, a, b), f"{case} gradient {i}")
 
 
 def test_weight_gradient_zero_upstream_leaves_buffer_bitwise():

@@ -128,45 +128,65 @@ namespace {
 
 // Balanced accumulation plan for an [m, n] output with k-reduction k on `workers` CUs:
 // whole rounds of 256 x 256 tiles run data-parallel, the other tiles' k-tiles are shared
-// evenly (stream-K) with at most `pieces` pieces per tile.
+// evenly (stream-K) by sk_workers = min(workers, units) workers, so that every share holds
+// at least one unit, with at most `pieces` pieces per tile.
 struct BalancedPlan {
-  int tiles_m, tiles_n, tiles, k_tiles, dp_tiles, sk_tiles, pieces;
+  int tiles_m, tiles_n, tiles, k_tiles, dp_tiles, sk_tiles, pieces, sk_workers;
   long units;
   long workspace_floats() const { return (long)sk_tiles * pieces * kFBM * kFBN; }
 };
 
-BalancedPlan balanced_plan(long m, long n, long k, int workers) {
+BalancedPlan balanced_plan_tiles(long tiles, long k, int workers) {
   BalancedPlan b{};
-  b.tiles_m = cdiv(m, kFBM);
-  b.tiles_n = cdiv(n, kFBN);
-  b.tiles = b.tiles_m * b.tiles_n;
+  b.tiles = (int)tiles;
   b.k_tiles = cdiv(k, kFBK);
   b.dp_tiles = b.tiles / workers * workers;
   b.sk_tiles = b.tiles - b.dp_tiles;
   b.units = (long)b.sk_tiles * b.k_tiles;
+  b.sk_workers = (int)(b.units < workers ? b.units : workers);
   b.pieces = 0;
   for (long ti = 0; ti < b.sk_tiles; ++ti) {
-    const int pc = sk_pieces_of(ti, b.k_tiles, b.units, workers);
+    const int pc = sk_pieces_of(ti, b.k_tiles, b.units, b.sk_workers);
     if (pc > b.pieces) b.pieces = pc;
   }
   return b;
 }
 
+BalancedPlan balanced_plan(long m, long n, long k, int workers) {
+  BalancedPlan b = balanced_plan_tiles(cdiv(m, kFBM) * cdiv(n, kFBN), k, workers);
+  b.tiles_m = cdiv(m, kFBM);
+  b.tiles_n = cdiv(n, kFBN);
+  return b;
+}
+
+// Outputs of a balanced accumulation: one GEMM, or the members of a grouped launch.
+struct SkOutputs {
+  int count;
+  GemmMember m[kMaxGroup];
+};
+
 // G[m, n] += f32(r(sum of the tile's pieces)) for the stream-K tiles of a balanced
 // accumulation: block (tile ti, chunk) handles 1024 elements of tile ti's 256 x 256 block,
-// four consecutive columns per thread; pieces are added in k order.
+// four consecutive columns per thread; pieces are added in k order. Tile ti is launch
+// raster index dp_tiles + ti, in the output of the member whose tiles hold it.
 __global__ void __launch_bounds__(256) sk_accum_kernel(const float* __restrict__ ws,
-                                                       float* __restrict__ g, long ldg, int M,
-                                                       int N, int tiles_m, int tiles_n,
-                                                       int dp_tiles, int k_tiles, long units,
-                                                       int workers, int pieces_max,
-                                                       int round_acc, int vec) {
+                                                       const SkOutputs out, int dp_tiles,
+                                                       int k_tiles, long units, int workers,
+                                                       int pieces_max, int round_acc, int vec) {
   const long ti = blockIdx.x / 64;
   const int e = (blockIdx.x % 64) * 1024 + threadIdx.x * 4;
   const int r = e / kFBN, c = e % kFBN;
+  const int t = dp_tiles + (int)ti;
+  GemmMember q = out.m[0];
+#pragma unroll
+  for (int i = 1; i < kMaxGroup; ++i)
+    if (i < out.count && t >= out.m[i].tile_base) q = out.m[i];
   int tm, tn;
-  tile_position(dp_tiles + (int)ti, tiles_m, tiles_n, tm, tn);
+  tile_position(t - q.tile_base, q.tiles_m, q.tiles_n, tm, tn);
   const int m = tm * kFBM + r, n = tn * kFBN + c;
+  const int M = q.M, N = q.N;
+  float* __restrict__ g = q.g;
+  const long ldg = q.ldg;
   if (m >= M || n >= N) return;
   const int pieces = sk_pieces_of(ti, k_tiles, units, workers);
   const float* src = ws + ti * pieces_max * (long)(kFBM * kFBN) + e;
@@ -235,10 +255,12 @@ extern "C" int ws_mm_accumulate_f32(const void* a, int64_t a_s0, int64_t a_s1, c
     p.sk_ws = workspace;
     if (int rc = dispatch_fast<false, FEpiAccF32<false>>(p, am, bm, LaunchCfg{1, 1, workers}, s))
       return rc;
+    SkOutputs out{};
+    out.count = 1;
+    out.m[0] = GemmMember{p.a, p.b, (int)m, (int)n, plan.tiles_m, plan.tiles_n, 0, g, (long)ldg};
     hipLaunchKernelGGL(sk_accum_kernel, dim3((unsigned)(plan.sk_tiles * 64)), dim3(256), 0, s,
-                       workspace, g, (long)ldg, (int)m, (int)n, plan.tiles_m, plan.tiles_n,
-                       plan.dp_tiles, plan.k_tiles, plan.units, workers, plan.pieces,
-                       round_bf16 ? 1 : 0, p.vec_out);
+                       workspace, out, plan.dp_tiles, plan.k_tiles, plan.units, plan.sk_workers,
+                       plan.pieces, round_bf16 ? 1 : 0, p.vec_out);
     return hip_check(hipGetLastError(), "stream-K reduce launch");
   }
   // Fewer tiles than compute units, or generic layouts: even split-K slices through the
@@ -260,4 +282,139 @@ extern "C" int ws_mm_accumulate_f32(const void* a, int64_t a_s0, int64_t a_s1, c
                      workspace, (int)splits, (long)(m * n), g, (long)ldg, (int)m, (int)n,
                      round_bf16 ? 1 : 0, vec);
   return hip_check(hipGetLastError(), "split-K reduce launch");
+}
+
+namespace {
+
+// Split count for one GEMM of a grouped call that falls back to single launches: the one
+// (fewest on ties, at most 4, each split at least 16 k-tiles) that best fills the last
+// round of 256 x 256 tiles.
+int auto_splits(long m, long n, long k, int cus) {
+  const long tiles = cdiv(m, kFBM) * cdiv(n, kFBN);
+  int best = 1;
+  double best_eff = 0.0;
+  for (int s = 1; s <= 4; ++s) {
+    if (s > 1 && cdiv(k, kFBK) / s < 16) break;
+    const long work = tiles * s;
+    const double eff = (double)work / (double)(cdiv(work, cus) * cus);
+    if (eff > best_eff + 1e-9) {
+      best = s;
+      best_eff = eff;
+    }
+  }
+  return best;
+}
+
+long group_tiles(const ws_accumulate_problem* pr, int count) {
+  long t = 0;
+  for (int i = 0; i < count; ++i) t += cdiv(pr[i].m, kFBM) * cdiv(pr[i].n, kFBN);
+  return t;
+}
+
+}  // namespace
+
+extern "C" int64_t ws_mm_accumulate_group_workspace_floats(const ws_accumulate_problem* problems,
+                                                           int count, int64_t k) {
+  if (!problems || count < 1 || count > kMaxGroup || k < 1) return 0;
+  const int workers = device_cus();
+  // The one-launch plan (used only when its tiles fill at least one round), or a fallback
+  // single call's split.
+  const BalancedPlan plan = balanced_plan_tiles(group_tiles(problems, count), k, workers);
+  long need = plan.dp_tiles > 0 ? plan.workspace_floats() : 0;
+  for (int i = 0; i < count; ++i) {
+    const long m = problems[i].m, n = problems[i].n;
+    if (m < 1 || n < 1) return 0;
+    const long one = ws_mm_accumulate_workspace_floats(m, n, k, auto_splits(m, n, k, workers));
+    if (one > need) need = one;
+  }
+  return need;
+}
+
+extern "C" int ws_mm_accumulate_f32_group(const ws_accumulate_problem* problems, int count,
+                                          int64_t k, int round_bf16, float* workspace,
+                                          void* stream) {
+  if (!problems) return set_error(kInvalid, "null problem table");
+  if (count < 1 || count > kMaxGroup)
+    return set_error(kInvalid, "group size %d outside [1, %d]", count, kMaxGroup);
+  for (int i = 0; i < count; ++i) {
+    const ws_accumulate_problem& q = problems[i];
+    if (int rc = check_gemm_args(q.a, q.a_s0, q.a_s1, q.b, q.b_s0, q.b_s1, q.g, q.m, q.n, k))
+      return rc;
+    if (q.ldg < q.n) return set_error(kInvalid, "gradient %d leading dimension %ld < n", i, (long)q.ldg);
+    if (int rc = check_out_stride(q.ldg, 4, "gradient")) return rc;
+  }
+  // The gradients are updated in place by different workgroups: they must not overlap.
+  for (int i = 0; i < count; ++i)
+    for (int j = i + 1; j < count; ++j) {
+      const char* bi = reinterpret_cast<const char*>(problems[i].g);
+      const char* bj = reinterpret_cast<const char*>(problems[j].g);
+      const long si = ((problems[i].m - 1) * problems[i].ldg + problems[i].n) * 4;
+      const long sj = ((problems[j].m - 1) * problems[j].ldg + problems[j].n) * 4;
+      if (bi < bj + sj && bj < bi + si)
+        return set_error(kInvalid, "gradients %d and %d overlap", i, j);
+    }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int workers = device_cus();
+  const BalancedPlan plan = balanced_plan_tiles(group_tiles(problems, count), k, workers);
+
+  // One launch when every GEMM takes the fast loader with the same operand layouts and
+  // vector outputs, and the tiles fill at least one round.
+  GemmParams p{};
+  p.K = (int)k;
+  p.round_acc = round_bf16 ? 1 : 0;
+  p.vec_out = 1;
+  int am = -1, bm = -1;
+  bool one_launch = plan.dp_tiles > 0 && (plan.sk_tiles == 0 || (workspace && al(workspace, 16)));
+  int base = 0;
+  for (int i = 0; i < count && one_launch; ++i) {
+    const ws_accumulate_problem& q = problems[i];
+    GemmParams pi{};
+    pi.a = desc_a(q.a, q.a_s0, q.a_s1);
+    pi.b = desc_b(q.b, q.b_s0, q.b_s1);
+    pi.vec_out = (q.n % 4 == 0) && (q.ldg % 4 == 0) && al(q.g, 16);
+    const int ami = operand_mode(pi.a, q.m, k, 256), bmi = operand_mode(pi.b, q.n, k, 256);
+    if (i == 0) {
+      am = ami;
+      bm = bmi;
+    }
+    if (ami != am || bmi != bm || !fast_ok(pi, ami, bmi, false)) {
+      one_launch = false;
+      break;
+    }
+    const int tm = cdiv(q.m, kFBM), tn = cdiv(q.n, kFBN);
+    p.grp[i] = GemmMember{pi.a, pi.b, (int)q.m, (int)q.n, tm, tn, base, q.g, (long)q.ldg};
+    base += tm * tn;
+  }
+  if (!one_launch) {
+    for (int i = 0; i < count; ++i) {
+      const ws_accumulate_problem& q = problems[i];
+      const int splits = workspace ? auto_splits(q.m, q.n, k, workers) : 1;
+      if (int rc = ws_mm_accumulate_f32(q.a, q.a_s0, q.a_s1, q.b, q.b_s0, q.b_s1, q.g, q.ldg, q.m,
+                                        q.n, k, round_bf16, workspace, splits, stream))
+        return rc;
+    }
+    return kOk;
+  }
+  p.group_count = count;
+  p.a = p.grp[0].a;
+  p.b = p.grp[0].b;
+  p.M = p.grp[0].M;
+  p.N = p.grp[0].N;
+  p.balanced = 1;
+  p.dp_tiles = plan.dp_tiles;
+  p.sk_tiles = plan.sk_tiles;
+  p.k_tiles = plan.k_tiles;
+  p.sk_units = plan.units;
+  p.sk_pieces = plan.pieces;
+  p.sk_ws = workspace;
+  if (int rc = dispatch_fast<false, FEpiAccF32<false>>(p, am, bm, LaunchCfg{1, 1, workers}, s))
+    return rc;
+  if (plan.sk_tiles == 0) return kOk;
+  SkOutputs out{};
+  out.count = count;
+  for (int i = 0; i < count; ++i) out.m[i] = p.grp[i];
+  hipLaunchKernelGGL(sk_accum_kernel, dim3((unsigned)(plan.sk_tiles * 64)), dim3(256), 0, s,
+                     workspace, out, plan.dp_tiles, plan.k_tiles, plan.units, plan.sk_workers,
+                     plan.pieces, round_bf16 ? 1 : 0, 1);
+  return hip_check(hipGetLastError(), "stream-K reduce launch");
 }

@@ -50,6 +50,15 @@ struct OperandDesc {
   long s_k;                   // stride along the reduction dim, elements
 };
 
+// One GEMM of a grouped FP32 accumulation: G[M, N] += A[M, K] B[K, N], its tiles at
+// raster indices [tile_base, tile_base + tiles_m * tiles_n) of the launch.
+struct GemmMember {
+  OperandDesc a, b;
+  int M, N, tiles_m, tiles_n, tile_base;
+  float* g; long ldg;
+};
+constexpr int kMaxGroup = 4;
+
 struct GemmParams {
   OperandDesc a, b;
   int M, N, K;       // logical sizes; for the paired SwiGLU GEMM N is the packed width 2H
@@ -79,6 +88,11 @@ struct GemmParams {
   int dp_tiles, sk_tiles, k_tiles, sk_pieces;
   long sk_units;
   float* sk_ws;
+  // Grouped balanced accumulation: group_count > 0 GEMMs sharing K, the operand layouts
+  // and round_acc, their rasters concatenated in member order (a, b, M, N, g, ldg and the
+  // tile counts above are then unused).
+  int group_count;
+  GemmMember grp[kMaxGroup];
 };
 
 // --------------------------------------------------------------------------------------

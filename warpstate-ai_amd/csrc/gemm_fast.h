@@ -393,25 +393,32 @@ struct FEpiAccF32 {
   __device__ __forceinline__ static void run(const GemmParams& p, Acc16<FA, FB>& acc, int m_base,
                                              int n_base, int lane, int tm, int tn, int wn,
                                              unsigned char* stage) {
+    add(p.g + (SPLIT ? (long)blockIdx.y * p.split_stride : 0), p.ldg, p.M, p.N, p.round_acc, acc,
+        m_base, n_base, lane, tm, tn);
+  }
+  // The tile's accumulators into the [M, N] output g (row stride ldg).
+  template <int FA, int FB>
+  __device__ __forceinline__ static void add(float* g, long ldg, int M, int N, int round_acc,
+                                             Acc16<FA, FB>& acc, int m_base, int n_base, int lane,
+                                             int tm, int tn) {
     opaque_lane(lane);
     const int m0 = tm * kFBM, n0 = tn * kFBN;
-    float* gbase = p.g + (SPLIT ? (long)blockIdx.y * p.split_stride : 0) + (long)m0 * p.ldg + n0;
-    __amdgpu_buffer_rsrc_t rg = make_rsrc(gbase, 0x7fffffff);
+    __amdgpu_buffer_rsrc_t rg = make_rsrc(g + (long)m0 * ldg + n0, 0x7fffffff);
 #pragma unroll
     for (int i = 0; i < FA; ++i) {
       const int m = m_base + 16 * i + (lane & 15);
-      const bool mok = m < p.M;
+      const bool mok = m < M;
 #pragma unroll
       for (int j = 0; j < FB; ++j) {
         const int n = n_base + 16 * j + 4 * (lane >> 4);
         {
-          const bool ok = mok && (n + 3 < p.N);
-          const unsigned off = store_off(ok, (long)(m - m0) * p.ldg + (n - n0), 4);
+          const bool ok = mok && (n + 3 < N);
+          const unsigned off = store_off(ok, (long)(m - m0) * ldg + (n - n0), 4);
           f32x4_t add;
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const float x = acc.v[i][j][e];
-            add[e] = (!SPLIT && p.round_acc) ? rbf16(x) : x;
+            add[e] = (!SPLIT && round_acc) ? rbf16(x) : x;
           }
           if (!SPLIT) {
             f32x4_t old = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rg, off, 0, 0));
@@ -581,15 +588,16 @@ __global__ void __launch_bounds__(kFNT) gemm_fast_kernel(const GemmParams p) {
     else b_rb[j] = wn * TN + 16 * j;
   }
 
-  // One output tile (raster index t) over k-tiles [kb, ke), then `epi(acc, m_base, n_base,
-  // tm, tn)` and a barrier (the next tile's loads reuse the epilogue's staging space).
-  auto run_tile = [&](int t, int kb, int ke, auto&& epi) {
+  // One output tile (raster index t of GEMM q) over k-tiles [kb, ke), then `epi(acc,
+  // m_base, n_base, tm, tn)` and a barrier (the next tile's loads reuse the epilogue's
+  // staging space).
+  auto run_tile = [&](const GemmMember& q, int t, int kb, int ke, auto&& epi) {
     int tm, tn;
-    tile_position(t, p.tiles_m, p.tiles_n, tm, tn);
+    tile_position(t, q.tiles_m, q.tiles_n, tm, tn);
     const int row0_a = tm * kFBM;
     const int row0_b = tn * bn_cols;
-    la.init(p.a, row0_a, p.M, 0, wave, lane);
-    lb.init(p.b, row0_b, PAIRED ? p.H : p.N, PAIRED ? p.H : 0, wave, lane);
+    la.init(q.a, row0_a, q.M, 0, wave, lane);
+    lb.init(q.b, row0_b, PAIRED ? p.H : q.N, PAIRED ? p.H : 0, wave, lane);
 
     Acc16<FA, FB> acc;
 #pragma unroll
@@ -598,16 +606,16 @@ __global__ void __launch_bounds__(kFNT) gemm_fast_kernel(const GemmParams p) {
       for (int j = 0; j < FB; ++j) acc.v[i][j] = f32x4_v{0.f, 0.f, 0.f, 0.f};
 
     if (kb < ke) {
-      la.issue(p.a, row0_a, kb * kFBK, p.K, fsmem, wave, lane);
-      lb.issue(p.b, row0_b, kb * kFBK, p.K, fsmem + kFTileBytes, wave, lane);
+      la.issue(q.a, row0_a, kb * kFBK, p.K, fsmem, wave, lane);
+      lb.issue(q.b, row0_b, kb * kFBK, p.K, fsmem + kFTileBytes, wave, lane);
       for (int kt = kb; kt < ke; ++kt) {
         const int cur = (kt - kb) & 1;
         __builtin_amdgcn_s_waitcnt(wait_vmcnt(0));
         __builtin_amdgcn_s_barrier();
         if (!kMidIssue && kt + 1 < ke) {
           unsigned char* nxt = fsmem + (cur ^ 1) * kFStageBytes;
-          la.issue(p.a, row0_a, (kt + 1) * kFBK, p.K, nxt, wave, lane);
-          lb.issue(p.b, row0_b, (kt + 1) * kFBK, p.K, nxt + kFTileBytes, wave, lane);
+          la.issue(q.a, row0_a, (kt + 1) * kFBK, p.K, nxt, wave, lane);
+          lb.issue(q.b, row0_b, (kt + 1) * kFBK, p.K, nxt + kFTileBytes, wave, lane);
         }
         const unsigned char* sa = fsmem + cur * kFStageBytes;
         const unsigned char* sb = sa + kFTileBytes;
@@ -631,8 +639,8 @@ __global__ void __launch_bounds__(kFNT) gemm_fast_kernel(const GemmParams p) {
             __builtin_amdgcn_sched_barrier(0);
             if (kt + 1 < ke) {
               unsigned char* nxt = fsmem + (cur ^ 1) * kFStageBytes;
-              la.issue(p.a, row0_a, (kt + 1) * kFBK, p.K, nxt, wave, lane);
-              lb.issue(p.b, row0_b, (kt + 1) * kFBK, p.K, nxt + kFTileBytes, wave, lane);
+              la.issue(q.a, row0_a, (kt + 1) * kFBK, p.K, nxt, wave, lane);
+              lb.issue(q.b, row0_b, (kt + 1) * kFBK, p.K, nxt + kFTileBytes, wave, lane);
             }
             __builtin_amdgcn_sched_barrier(0);
           }
@@ -671,29 +679,49 @@ __global__ void __launch_bounds__(kFNT) gemm_fast_kernel(const GemmParams p) {
     epi(acc, m_base, n_base, tm, tn);
     __builtin_amdgcn_s_barrier();
   };
+  const GemmMember self{p.a, p.b, p.M, p.N, p.tiles_m, p.tiles_n, 0, p.g, p.ldg};
   if constexpr (std::is_same<Epi, FEpiAccF32<false>>::value) {
     // Balanced accumulation (the other instantiations use the plain tile loop below).
     if (p.balanced) {
+      // The GEMM that launch raster index t belongs to (uniform selects over the member
+      // table of a grouped launch).
+      auto member = [&](int t) {
+        if (p.group_count == 0) return self;
+        GemmMember q = p.grp[0];
+#pragma unroll
+        for (int i = 1; i < kMaxGroup; ++i)
+          if (i < p.group_count && t >= p.grp[i].tile_base) q = p.grp[i];
+        return q;
+      };
       // Whole tiles, accumulated straight into G.
-      for (int w = blockIdx.x; w < p.dp_tiles; w += gridDim.x)
-        run_tile(xcd_remap(w, p.dp_tiles, gridDim.x), 0, p.k_tiles,
+      for (int w = blockIdx.x; w < p.dp_tiles; w += gridDim.x) {
+        const int t = xcd_remap(w, p.dp_tiles, gridDim.x);
+        const GemmMember q = member(t);
+        run_tile(q, t - q.tile_base, 0, p.k_tiles,
                  [&](auto& acc, int m_base, int n_base, int tm, int tn) {
-                   Epi::run(p, acc, m_base, n_base, lane, tm, tn, wn, fsmem + wave * kFStageWave);
+                   // Selected again here, so that only t stays live across the k-loop.
+                   const GemmMember o = member(t);
+                   Epi::add(o.g, o.ldg, o.M, o.N, p.round_acc, acc, m_base, n_base, lane, tm, tn);
                  });
+      }
       // This workgroup's stream-K share of the remaining tiles' k-tiles. Worker indices
       // run XCD-contiguous (the dispatcher deals workgroups round-robin to the XCDs) so
-      // that the pieces running together on one XCD belong to neighbouring tiles.
-      const long W = gridDim.x, b = blockIdx.x;
-      const long v = W % kXcds == 0 ? (b % kXcds) * (W / kXcds) + b / kXcds : b;
-      long x = sk_begin(v, p.sk_units, W);
-      const long end = sk_begin(v + 1, p.sk_units, W);
+      // that the pieces running together on one XCD belong to neighbouring tiles. With
+      // fewer units than workgroups only the first sk_units workers take a share, so that
+      // no share is empty and a tile's pieces are numbered without gaps.
+      const long G = gridDim.x, b = blockIdx.x;
+      const long v = G % kXcds == 0 ? (b % kXcds) * (G / kXcds) + b / kXcds : b;
+      const long W = min(G, p.sk_units);
+      long x = v < W ? sk_begin(v, p.sk_units, W) : 0;
+      const long end = v < W ? sk_begin(v + 1, p.sk_units, W) : 0;
       while (x < end) {
         const long ti = x / p.k_tiles;
         const int kb = (int)(x - ti * p.k_tiles);
         const int ke = (int)min((long)p.k_tiles, kb + (end - x));
         const long piece = v - sk_worker(ti * p.k_tiles, p.sk_units, W);
         float* block = p.sk_ws + (ti * p.sk_pieces + piece) * (long)(kFBM * kFBN);
-        run_tile(p.dp_tiles + (int)ti, kb, ke,
+        const GemmMember q = member(p.dp_tiles + (int)ti);
+        run_tile(q, p.dp_tiles + (int)ti - q.tile_base, kb, ke,
                  [&](auto& acc, int m_base, int n_base, int tm, int tn) {
                    FEpiPartial::run(acc, m_base - tm * kFBM, n_base - tn * kFBN, lane, block);
                  });
@@ -703,7 +731,7 @@ __global__ void __launch_bounds__(kFNT) gemm_fast_kernel(const GemmParams p) {
     }
   }
   for (int w = blockIdx.x; w < p.total_tiles; w += gridDim.x)
-    run_tile(xcd_remap(w, p.total_tiles, gridDim.x), kt_begin, kt_end,
+    run_tile(self, xcd_remap(w, p.total_tiles, gridDim.x), kt_begin, kt_end,
              [&](auto& acc, int m_base, int n_base, int tm, int tn) {
                Epi::run(p, acc, m_base, n_base, lane, tm, tn, wn, fsmem + wave * kFStageWave);
              });

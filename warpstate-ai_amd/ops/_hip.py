@@ -50,6 +50,8 @@ SIGNATURES = {
     "ws_mm_accumulate_workspace_floats": (_i64, [_i64, _i64, _i64, _i64]),
     "ws_mm_accumulate_f32": (_i32, [_c_void_p, _i64, _i64, _c_void_p, _i64, _i64, _c_void_p, _i64,
                                     _i64, _i64, _i64, _i32, _c_void_p, _i64, _c_void_p]),
+    "ws_mm_accumulate_group_workspace_floats": (_i64, [_c_void_p, _i32, _i64]),
+    "ws_mm_accumulate_f32_group": (_i32, [_c_void_p, _i32, _i64, _i32, _c_void_p, _c_void_p]),
     "ws_linear_ce_parts": (_i64, [_i64]),
     "ws_linear_ce_forward": (_i32, [_c_void_p, _i64, _c_void_p, _i64, _c_void_p, _i64, _i64, _i64,
                                     _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
@@ -62,6 +64,20 @@ SIGNATURES = {
     "ws_backward_layout": (_i32, [_c_void_p] * 15 + [_i64] * 5 + [_f32, _i32, _c_void_p,
                                                                    _c_void_p, _c_void_p]),
 }
+
+
+class AccumulateProblem(ctypes.Structure):
+    """``ws_accumulate_problem``: one weight gradient of a grouped accumulation."""
+    _fields_ = [("a", _c_void_p), ("a_s0", _i64), ("a_s1", _i64),
+                ("b", _c_void_p), ("b_s0", _i64), ("b_s1", _i64),
+                ("g", _c_void_p), ("ldg", _i64), ("m", _i64), ("n", _i64)]
+
+
+def problem_table(rows) -> ctypes.Array:
+    """A ``ws_accumulate_problem`` array from (a, a_s0, a_s1, b, b_s0, b_s1, g, ldg, m, n)
+    tuples of pointers and element counts."""
+    return (AccumulateProblem * len(rows))(*[AccumulateProblem(*r) for r in rows])
+
 
 _lock = threading.Lock()
 _library = None

@@ -232,6 +232,39 @@ def mm_accumulate_(g: torch.Tensor, a: torch.Tensor, b: torch.Tensor, round_bf16
     return g
 
 
+def mm_accumulate_group_(items, round_bf16: bool = True,
+                         workspace: torch.Tensor | None = None) -> None:
+    """G_i += f32(r(a_i @ b_i)) for up to four (G_i, a_i, b_i) with the same reduction
+    length, in place and in one launch (``ws_mm_accumulate_f32_group``): the tiles of all
+    gradients share the GPU, so a gradient with fewer 256 x 256 tiles than compute units
+    does not leave the rest idle. Each G_i is FP32 with unit column stride; the G_i must
+    not overlap."""
+    rows = []
+    k = None
+    for g, a, b in items:
+        _check_bf16_cuda(a, b)
+        if g.dtype != torch.float32 or g.stride(1) != 1:
+            raise ValueError("Gradient buffer must be FP32 with unit column stride")
+        m, ka = a.shape
+        n = b.shape[1]
+        if g.shape != (m, n) or b.shape[0] != ka:
+            raise ValueError("Gradient buffer shape must match a @ b")
+        if k is not None and ka != k:
+            raise ValueError("Grouped gradients must share the reduction length")
+        k = ka
+        rows.append((a.data_ptr(), a.stride(0), a.stride(1), b.data_ptr(), b.stride(0),
+                     b.stride(1), g.data_ptr(), g.stride(0), m, n))
+    if not rows:
+        return
+    table = _hip.problem_table(rows)
+    first = items[0][0]
+    need = _hip.query("ws_mm_accumulate_group_workspace_floats", table, len(rows), k)
+    if need and (workspace is None or workspace.numel() < need):
+        workspace = torch.empty((need,), dtype=torch.float32, device=first.device)
+    _hip.call("ws_mm_accumulate_f32_group", table, len(rows), k, int(round_bf16),
+              None if not need else workspace.data_ptr(), _hip.stream(items[0][1]))
+
+
 class CrossEntropyState:
     """Per-call buffers of the fused LM-head cross-entropy."""
 
@@ -361,6 +394,10 @@ def mlp_backward(x: torch.Tensor, w_upgate: torch.Tensor, w_down: torch.Tensor,
     """
     dpacked = swiglu_backward_mm(dy, w_down, packed, eager_rounding)
     dx = mm(dpacked, w_upgate)
-    mm_accumulate_(g_down, dy.T, act, True, dw_splits)
-    mm_accumulate_(g_upgate, dpacked.T, x, True, dw_splits)
+    if dw_splits is None:
+        # Both weight gradients reduce over the tokens: one launch fills the GPU with them.
+        mm_accumulate_group_([(g_down, dy.T, act), (g_upgate, dpacked.T, x)], True)
+    else:
+        mm_accumulate_(g_down, dy.T, act, True, dw_splits)
+        mm_accumulate_(g_upgate, dpacked.T, x, True, dw_splits)
     return dx
