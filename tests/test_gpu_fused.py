@@ -62,7 +62,9 @@ def test_swiglu_zero_gate_weights_give_exact_zero():
 
 
 @pytest.mark.parametrize("m,d,n,gate", [(512, 256, 576, (384, 512)), (300, 2048, 1152, (768, 1024)),
-                                        (1024, 2048, 9216, (6144, 8192))])
+                                        (1024, 2048, 9216, (6144, 8192)),
+                                        # rows held in registers with a partial last chunk
+                                        (200, 1000, 512, (256, 512)), (130, 3072, 512, (0, 256))])
 def test_rmsnorm_gate_projection(m, d, n, gate):
     from ops.benchmark_configs import rms_projection_inputs
     from ops.fused_execution import rmsnorm_gate_mm

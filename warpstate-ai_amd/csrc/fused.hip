@@ -51,9 +51,24 @@ extern "C" int ws_rmsnorm_gate_mm(const void* x, int64_t x_s0, const float* norm
   hipStream_t s = static_cast<hipStream_t>(stream);
   // Prologue: one pass over x writes the normalized BF16 operand y and rstd.
   const int vec = (x_s0 % 8 == 0) && (k % 8 == 0) && al(x, 16) && al(normed, 16);
-  hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(cdiv(m, 4)), dim3(256), 0, s,
-                     static_cast<const unsigned short*>(x), (long)x_s0, norm_weight,
-                     static_cast<unsigned short*>(normed), rstd, (int)m, (int)k, eps, vec);
+  const dim3 rgrid(cdiv(m, 4));
+  const auto* xs = static_cast<const unsigned short*>(x);
+  auto* ys = static_cast<unsigned short*>(normed);
+  if (vec && k <= 512)
+    hipLaunchKernelGGL(rmsnorm_rows_reg_kernel<1>, rgrid, dim3(256), 0, s, xs, (long)x_s0,
+                       norm_weight, ys, rstd, (int)m, (int)k, eps);
+  else if (vec && k <= 1024)
+    hipLaunchKernelGGL(rmsnorm_rows_reg_kernel<2>, rgrid, dim3(256), 0, s, xs, (long)x_s0,
+                       norm_weight, ys, rstd, (int)m, (int)k, eps);
+  else if (vec && k <= 2048)
+    hipLaunchKernelGGL(rmsnorm_rows_reg_kernel<4>, rgrid, dim3(256), 0, s, xs, (long)x_s0,
+                       norm_weight, ys, rstd, (int)m, (int)k, eps);
+  else if (vec && k <= 4096)
+    hipLaunchKernelGGL(rmsnorm_rows_reg_kernel<8>, rgrid, dim3(256), 0, s, xs, (long)x_s0,
+                       norm_weight, ys, rstd, (int)m, (int)k, eps);
+  else
+    hipLaunchKernelGGL(rmsnorm_rows_kernel, rgrid, dim3(256), 0, s, xs, (long)x_s0, norm_weight,
+                       ys, rstd, (int)m, (int)k, eps, vec);
   if (int rc = hip_check(hipGetLastError(), "rmsnorm rows launch")) return rc;
   GemmParams p{};
   p.a = desc_a(normed, k, 1);

@@ -94,6 +94,53 @@ static __global__ void __launch_bounds__(256) rmsnorm_rows_kernel(
   if (lane == 0) rstd[row] = r;
 }
 
+// rmsnorm_rows_kernel for vector rows of at most 512 NC elements: each lane keeps its NC
+// 16-byte chunks of the row in registers (all loads in flight at once), so x is read
+// once. Same sums in the same order, so the same bits as rmsnorm_rows_kernel.
+template <int NC>
+static __global__ void __launch_bounds__(256) rmsnorm_rows_reg_kernel(
+    const unsigned short* __restrict__ x, long ldx, const float* __restrict__ w,
+    unsigned short* __restrict__ y, float* __restrict__ rstd, int rows, int D, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const unsigned short* xr = x + (long)row * ldx;
+  unsigned short* yr = y + (long)row * D;
+  u32x4_t v[NC];
+#pragma unroll
+  for (int i = 0; i < NC; ++i) {
+    const int c = lane * 8 + i * 512;
+    v[i] = c < D ? *reinterpret_cast<const u32x4_t*>(xr + c) : u32x4_t{0, 0, 0, 0};
+  }
+  float acc = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NC; ++i)
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      const float a = lo_bf16(v[i][d]), b = hi_bf16(v[i][d]);
+      acc += a * a;
+      acc += b * b;
+    }
+  acc = wave_sum(acc);
+  const float r = 1.0f / sqrtf(acc / (float)D + eps);
+#pragma unroll
+  for (int i = 0; i < NC; ++i) {
+    const int c = lane * 8 + i * 512;
+    if (c >= D) break;
+    const f32x4_t w0 = *reinterpret_cast<const f32x4_t*>(w + c);
+    const f32x4_t w1 = *reinterpret_cast<const f32x4_t*>(w + c + 4);
+    const float wv[8] = {w0[0], w0[1], w0[2], w0[3], w1[0], w1[1], w1[2], w1[3]};
+    u32x4_t o;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      const float z0 = rbf16(lo_bf16(v[i][d]) * r), z1 = rbf16(hi_bf16(v[i][d]) * r);
+      o[d] = pack_bf16x2(z0 * rbf16(wv[2 * d]), z1 * rbf16(wv[2 * d + 1]));
+    }
+    *reinterpret_cast<u32x4_t*>(yr + c) = o;
+  }
+  if (lane == 0) rstd[row] = r;
+}
+
 // Standalone BF16 RMSNorm forward (ops/activation_execution.py:96-110): z = x * rstd,
 // y = z * w with z and w rounded to BF16 when eager; also stores rstd.
 static __global__ void __launch_bounds__(256) rmsnorm_fwd_kernel(const unsigned short* __restrict__ x,
