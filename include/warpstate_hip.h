@@ -196,14 +196,18 @@ int64_t ws_linear_ce_parts(int64_t vocab);
  * Fused LM-head cross-entropy forward. hidden [rows, d] (row stride ld_hidden, unit column
  * stride), weight [vocab, d] (nn.Embedding / tied head layout, row stride ld_weight),
  * int64 targets with -100 ignored. Writes per-token FP32 loss, lse, the target logit,
- * mean = sum(loss) / max(1, count) and count; logits exist only in registers.
+ * mean = sum(loss) / max(1, count) and count. `logits` (nullable): when given, the rounded
+ * BF16 logits are also stored there ([rows, vocab], row stride vocab; vocab % 4 == 0,
+ * 16-byte aligned; both operands row-contiguous) for a backward that reads them instead
+ * of recomputing the GEMM. Without it the logits exist only in registers.
  * Restates the chunked head of WarpStateLM.forward (warpstate/model.py:316-334) and
  * `_full_loss` (ops/loss_experiment.py:14-19).
  */
 int ws_linear_ce_forward(const void* hidden, int64_t ld_hidden, const void* weight,
                          int64_t ld_weight, const int64_t* targets, int64_t rows, int64_t vocab,
                          int64_t d, float* part_max, float* part_sum, float* target_logit,
-                         float* lse, float* loss, float* mean, float* count, void* stream);
+                         float* lse, float* loss, float* mean, float* count, void* logits,
+                         void* stream);
 
 /* Bytes of the workspace ws_linear_ce_backward needs for `chunk_rows`-row chunks. */
 int64_t ws_linear_ce_workspace_bytes(int64_t rows, int64_t vocab, int64_t d, int64_t chunk_rows);
@@ -219,7 +223,9 @@ int64_t ws_linear_ce_workspace_bytes(int64_t rows, int64_t vocab, int64_t d, int
  * [vocab, d], row stride ld_dweight) receives the tied head weight's gradient, accumulated
  * per chunk as dweight += f32(r(G_chunk^T @ hidden_chunk)): the BF16 weight gradient of the
  * chunk's F.linear followed by FP32 accumulation (warpstate/model.py:321-331 under BF16
- * autocast, test_gradient_execution.py:243-246). Restates autograd of
+ * autocast, test_gradient_execution.py:243-246). `logits` (nullable): the logits the
+ * forward stored; each chunk's logit gradients then come from one elementwise pass over
+ * them (same arithmetic, same bits) instead of a recomputing GEMM. Restates autograd of
  * warpstate/model.py:321-334.
  */
 int ws_linear_ce_backward(const void* hidden, int64_t ld_hidden, const void* weight,
@@ -227,7 +233,7 @@ int ws_linear_ce_backward(const void* hidden, int64_t ld_hidden, const void* wei
                           const float* lse, const float* count, const float* grad_mean,
                           int64_t rows, int64_t vocab, int64_t d, void* workspace,
                           int64_t chunk_rows, void* dhidden, int64_t ld_dhidden, float* dweight,
-                          int64_t ld_dweight, void* stream);
+                          int64_t ld_dweight, const void* logits, void* stream);
 
 /*
  * Packed attention-backward gradient layout: out [B, N*C, 5*H*D] BF16 (token-major rows of

@@ -128,3 +128,24 @@ def test_config5_lm_head_cross_entropy_full():
                           rtol=1e-6)
     assert abs(state.mean.item() - math.log(32768)) < 1e-5
     assert torch.count_nonzero(dh0).item() == 0
+
+
+def test_config5_stored_logits_match_the_recomputing_backward_bitwise():
+    """Config 5 with the logits kept by the forward (1 GiB of BF16): the backward's
+    elementwise logit gradients give the recomputing GEMM's dHidden bit for bit."""
+    from ops.fused_execution import (CrossEntropyState, linear_cross_entropy_backward,
+                                     linear_cross_entropy_forward)
+
+    inp = cfg.lm_head_inputs(seed=0)
+    hidden, weight, targets = (inp[k].cuda() for k in ("hidden", "weight", "targets"))
+    grad = torch.full((), 0.75, device="cuda")
+    got = []
+    for store in (False, True):
+        state = CrossEntropyState(hidden.shape[0], weight.shape[0], hidden.device,
+                                  store_logits=store)
+        linear_cross_entropy_forward(hidden, weight, targets, state)
+        got.append((state, linear_cross_entropy_backward(hidden, weight, targets, state, grad)))
+    torch.cuda.synchronize()
+    (a, dha), (b, dhb) = got
+    assert torch.equal(a.loss, b.loss) and torch.equal(a.lse, b.lse)
+    assert torch.equal(dha, dhb)

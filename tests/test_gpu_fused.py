@@ -351,6 +351,38 @@ def test_mlp_backward_matches_oracle():
     assert_f32_close(g_down.cpu(), want_gdown, "G_down")
 
 
+@pytest.mark.parametrize("rows,d,vocab,chunk", [(512, 256, 1024, 256), (3000, 384, 2052, 1024)])
+def test_linear_cross_entropy_stored_logits_match_recompute_bitwise(rows, d, vocab, chunk):
+    """The forward's stored BF16 logits are r(hidden @ W^T); the backward that reads them
+    gives the recomputing backward's loss, dHidden and head-weight gradient bit for bit
+    (2052 columns: a last 4-column piece in both the store and the gradient pass)."""
+    from ops.fused_execution import (CrossEntropyState, linear_cross_entropy_backward,
+                                     linear_cross_entropy_forward)
+
+    gen = _gen(404)
+    h = torch.randn(rows, d, generator=gen).bfloat16()
+    w = (torch.randn(vocab, d, generator=gen) * 0.05).bfloat16()
+    t = torch.randint(0, vocab, (rows,), generator=gen)
+    t[::7] = -100
+    hc, wc, tc = h.cuda(), w.cuda(), t.cuda()
+    grad = torch.full((), 0.7, device="cuda")
+    got = []
+    for store in (False, True):
+        state = CrossEntropyState(rows, vocab, hc.device, chunk_rows=chunk, store_logits=store)
+        linear_cross_entropy_forward(hc, wc, tc, state)
+        gw = torch.zeros(vocab, d, device="cuda")
+        dh = linear_cross_entropy_backward(hc, wc, tc, state, grad, weight_grad=gw)
+        got.append((state, dh, gw))
+    torch.cuda.synchronize()
+    (a, dha, gwa), (b, dhb, gwb) = got
+    for name in ("loss", "lse", "mean", "count"):
+        assert torch.equal(getattr(a, name), getattr(b, name)), name
+    valid = tc != -100  # the target logit is written for valid rows only
+    assert torch.equal(a.target_logit[valid], b.target_logit[valid])
+    assert torch.equal(dha, dhb) and torch.equal(gwa, gwb)
+    assert_bf16_close(b.logits, oracle.mm(h, w.T), "stored logits")
+
+
 @pytest.mark.parametrize("m,d,vocab,chunk", [(512, 256, 1024, 2048), (300, 512, 4096, 128),
                                              (1024, 2048, 8192, 512)])
 def test_linear_cross_entropy(m, d, vocab, chunk):

@@ -33,7 +33,7 @@ extern "C" int ws_linear_ce_forward(const void* hidden, int64_t ld_hidden, const
                                     int64_t ld_weight, const int64_t* targets, int64_t rows,
                                     int64_t vocab, int64_t d, float* part_max, float* part_sum,
                                     float* target_logit, float* lse, float* loss, float* mean,
-                                    float* count, void* stream) {
+                                    float* count, void* logits, void* stream) {
   if (int rc = check_ce(hidden, ld_hidden, weight, ld_weight, targets, rows, vocab, d)) return rc;
   if (!part_max || !part_sum || !target_logit || !lse || !loss || !mean || !count)
     return set_error(kInvalid, "null output pointer");
@@ -49,7 +49,18 @@ extern "C" int ws_linear_ce_forward(const void* hidden, int64_t ld_hidden, const
   p.parts_per_row = (int)ws_linear_ce_parts(vocab);
   p.vec_out = 1;  // the statistics epilogue stores no output tile
   int am = operand_mode(p.a, rows, d, 256), bm = operand_mode(p.b, vocab, d, 256);
-  if (fast_ok(p, am, bm, false)) {
+  if (logits) {
+    // The logits are kept for the backward: [rows, vocab] BF16, written by the fast path's
+    // staged epilogue.
+    if (vocab % 4 || reinterpret_cast<unsigned long>(logits) % 16)
+      return set_error(kInvalid, "stored logits need vocab %% 4 == 0 and a 16-byte aligned buffer");
+    if (int rc = check_out_stride(vocab, 2, "logits")) return rc;
+    if (!fast_ok(p, am, bm, false))
+      return set_error(kInvalid, "stored logits need row-contiguous hidden and weight operands");
+    p.c = static_cast<unsigned short*>(logits);
+    p.ldc = vocab;
+    if (int rc = dispatch_fast<false, FEpiCEStatsLogits>(p, am, bm, LaunchCfg{0, 1}, s)) return rc;
+  } else if (fast_ok(p, am, bm, false)) {
     if (int rc = dispatch_fast<false, FEpiCEStats>(p, am, bm, LaunchCfg{0, 1}, s)) return rc;
   } else if (int rc = dispatch<kMaskKK | kMaskGG, WS_TILE_ARGS_LARGE, false, false, EpiCEStats>(
                  p, am, bm, LaunchCfg{0, 1}, s)) {
@@ -91,7 +102,8 @@ extern "C" int ws_linear_ce_backward(const void* hidden, int64_t ld_hidden, cons
                                      const float* count, const float* grad_mean, int64_t rows,
                                      int64_t vocab, int64_t d, void* workspace,
                                      int64_t chunk_rows, void* dhidden, int64_t ld_dhidden,
-                                     float* dweight, int64_t ld_dweight, void* stream) {
+                                     float* dweight, int64_t ld_dweight, const void* logits,
+                                     void* stream) {
   if (int rc = check_ce(hidden, ld_hidden, weight, ld_weight, targets, rows, vocab, d)) return rc;
   if (!lse || !count || !grad_mean || !workspace || !dhidden) return set_error(kInvalid, "null pointer");
   if (chunk_rows < 1 || !fits_i32(chunk_rows * vocab)) return set_error(kInvalid, "bad chunk_rows");
@@ -99,6 +111,8 @@ extern "C" int ws_linear_ce_backward(const void* hidden, int64_t ld_hidden, cons
   if (dweight && ld_dweight < d) return set_error(kInvalid, "dweight leading dimension < d");
   if (reinterpret_cast<unsigned long>(workspace) % 256) return set_error(kInvalid, "workspace must be 256-byte aligned");
   if (int rc = check_out_stride(vocab, 2, "logit-gradient chunk")) return rc;
+  if (logits && (vocab % 4 || reinterpret_cast<unsigned long>(logits) % 16))
+    return set_error(kInvalid, "stored logits need vocab %% 4 == 0 and a 16-byte aligned buffer");
   if (int rc = check_out_stride(ld_dhidden, 2, "dhidden")) return rc;
   if (int rc = check_out_stride(d, 4, "dhidden partial")) return rc;
   if (dweight) {
@@ -127,7 +141,14 @@ extern "C" int ws_linear_ce_backward(const void* hidden, int64_t ld_hidden, cons
     p.lse = lse + start;
     p.grad_scale = scale_ws;
     int am = operand_mode(p.a, r, d, 256), bm = operand_mode(p.b, vocab, d, 256);
-    if (fast_ok(p, am, bm, false)) {
+    if (logits) {
+      // Logit gradients from the stored logits: one elementwise pass instead of the GEMM.
+      const long blocks = r * (long)cdiv(vocab, 2048);
+      hipLaunchKernelGGL(ce_grad_logits_kernel, dim3((unsigned)blocks), dim3(256), 0, s,
+                         static_cast<const unsigned short*>(logits) + start * vocab, (long)vocab,
+                         p.targets, p.lse, scale_ws, gl, (long)vocab, (int)r, (int)vocab);
+      if (int rc = hip_check(hipGetLastError(), "ce gradient launch")) return rc;
+    } else if (fast_ok(p, am, bm, false)) {
       if (int rc = dispatch_fast<false, FEpiCEGrad>(p, am, bm, LaunchCfg{0, 1}, s)) return rc;
     } else if (int rc = dispatch<kMaskKK | kMaskGG, WS_TILE_ARGS_LARGE, false, false, EpiCEGrad>(
                    p, am, bm, LaunchCfg{0, 1}, s)) {

@@ -549,6 +549,48 @@ struct FEpiCEGrad {
   }
 };
 
+// LM-head pass 1 that also keeps the logits: the statistics of FEpiCEStats, then the
+// rounded BF16 logits through the wave's LDS staging rows into c [M, N] (row stride ldc,
+// N % 4 == 0) as 16-byte row pieces, so that the backward reads them instead of
+// recomputing the GEMM.
+struct FEpiCEStatsLogits {
+  template <int FA, int FB>
+  __device__ __forceinline__ static void run(const GemmParams& p, Acc16<FA, FB>& acc, int m_base,
+                                             int n_base, int lane, int tm, int tn, int wn,
+                                             unsigned char* stage) {
+    static_assert(FA * 16 == 64 && FB * 16 == 128, "staging holds a 64 x 128 wave tile");
+    FEpiCEStats::run(p, acc, m_base, n_base, lane, tm, tn, wn, stage);  // acc now rounded
+    opaque_lane(lane);
+#pragma unroll
+    for (int i = 0; i < FA; ++i)
+#pragma unroll
+      for (int j = 0; j < FB; ++j) {
+        const int r = 16 * i + (lane & 15), c = 16 * j + 4 * (lane >> 4);
+        u32x2_t w = {pack_bf16x2(acc.v[i][j][0], acc.v[i][j][1]),
+                     pack_bf16x2(acc.v[i][j][2], acc.v[i][j][3])};
+        *reinterpret_cast<u32x2_t*>(stage + r * kFStageRow + c * 2) = w;
+      }
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's staging writes landed
+    const int c8 = 8 * (lane & 15);
+    const int n = n_base + c8;
+    const bool full = n + 7 < p.N, half = n + 3 < p.N;
+    __amdgpu_buffer_rsrc_t rc = make_rsrc(p.c + (long)m_base * p.ldc + n_base, 0x7fffffff);
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      const int r = 4 * q + (lane >> 4);
+      const bool ok = m_base + r < p.M;
+      const u32x4_t vl = *reinterpret_cast<const u32x4_t*>(stage + r * kFStageRow + c8 * 2);
+      const long off = (long)r * p.ldc + c8;
+      if (full) {
+        __builtin_amdgcn_raw_buffer_store_b128(vl, rc, store_off(ok, off, 2), 0, kEpiNT);
+      } else {
+        __builtin_amdgcn_raw_buffer_store_b64(u32x2_t{vl[0], vl[1]}, rc, store_off(ok && half, off, 2), 0, kEpiNT);
+      }
+    }
+  }
+};
+
 // --------------------------------------------------------------------------------------
 // The kernel.
 

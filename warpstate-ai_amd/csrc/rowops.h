@@ -560,3 +560,44 @@ static __global__ void __launch_bounds__(256) sigmoid_backward_cols_kernel(
 }
 
 }  // namespace ws
+
+namespace ws {
+
+// Logit gradients of one chunk from stored BF16 logits, with the arithmetic of the
+// LM-head pass 2 epilogue: g = r(scale * exp(l - lse) - [n == target] scale), scale = 0 for
+// ignored rows (target -100). Thread (row, 8-column piece) reads and writes 16 bytes;
+// vocab % 4 == 0, a last half piece moves 8 bytes.
+static __global__ void __launch_bounds__(256) ce_grad_logits_kernel(
+    const unsigned short* __restrict__ logits, long ld_logits, const long* __restrict__ targets,
+    const float* __restrict__ lse, const float* __restrict__ grad_scale,
+    unsigned short* __restrict__ g, long ldg, int rows, int vocab) {
+  const int per_row = (vocab + 2047) / 2048;  // blocks per row
+  const int m = blockIdx.x / per_row;
+  const int n = ((blockIdx.x % per_row) * 256 + threadIdx.x) * 8;
+  if (m >= rows || n >= vocab) return;
+  const long tgt = targets[m];
+  const float l0 = lse[m];
+  const float scale = (tgt == -100) ? 0.0f : *grad_scale;
+  const unsigned short* src = logits + (long)m * ld_logits + n;
+  unsigned short* dst = g + (long)m * ldg + n;
+  const bool full = n + 7 < vocab;
+  u32x4_t vl;
+  if (full) {
+    vl = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(src));
+  } else {
+    const u32x2_t h = *reinterpret_cast<const u32x2_t*>(src);
+    vl = u32x4_t{h[0], h[1], 0u, 0u};
+  }
+  u32x4_t o;
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    const long e = n + 2 * d;
+    const float v0 = scale * exp_e(lo_bf16(vl[d]) - l0) - (e == tgt ? scale : 0.0f);
+    const float v1 = scale * exp_e(hi_bf16(vl[d]) - l0) - (e + 1 == tgt ? scale : 0.0f);
+    o[d] = pack_bf16x2(v0, v1);
+  }
+  if (full) *reinterpret_cast<u32x4_t*>(dst) = o;
+  else *reinterpret_cast<u32x2_t*>(dst) = u32x2_t{o[0], o[1]};
+}
+
+}  // namespace ws

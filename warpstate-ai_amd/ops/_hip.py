@@ -55,12 +55,12 @@ SIGNATURES = {
     "ws_linear_ce_parts": (_i64, [_i64]),
     "ws_linear_ce_forward": (_i32, [_c_void_p, _i64, _c_void_p, _i64, _c_void_p, _i64, _i64, _i64,
                                     _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
-                                    _c_void_p, _c_void_p, _c_void_p]),
+                                    _c_void_p, _c_void_p, _c_void_p, _c_void_p]),
     "ws_linear_ce_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64]),
     "ws_linear_ce_backward": (_i32, [_c_void_p, _i64, _c_void_p, _i64, _c_void_p, _c_void_p,
                                      _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64,
                                      _c_void_p, _i64, _c_void_p, _i64, _c_void_p, _i64,
-                                     _c_void_p]),
+                                     _c_void_p, _c_void_p]),
     "ws_backward_layout": (_i32, [_c_void_p] * 15 + [_i64] * 5 + [_f32, _i32, _c_void_p,
                                                                    _c_void_p, _c_void_p]),
 }

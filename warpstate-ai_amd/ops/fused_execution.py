@@ -266,9 +266,12 @@ def mm_accumulate_group_(items, round_bf16: bool = True,
 
 
 class CrossEntropyState:
-    """Per-call buffers of the fused LM-head cross-entropy."""
+    """Per-call buffers of the fused LM-head cross-entropy. With ``store_logits`` the
+    forward also keeps the BF16 logits ([rows, vocab], 2 bytes each) and the backward
+    reads them instead of recomputing the logits GEMM."""
 
-    def __init__(self, rows, vocab, device, chunk_rows=DEFAULT_CE_CHUNK_ROWS, d=None):
+    def __init__(self, rows, vocab, device, chunk_rows=DEFAULT_CE_CHUNK_ROWS, d=None,
+                 store_logits=False):
         parts = _hip.query("ws_linear_ce_parts", vocab)
         f32 = dict(dtype=torch.float32, device=device)
         self.part_max = torch.empty((rows, parts), **f32)
@@ -280,6 +283,8 @@ class CrossEntropyState:
         self.count = torch.empty((), **f32)
         self.rows, self.vocab = rows, vocab
         self.chunk_rows = min(chunk_rows, rows)
+        self.logits = (torch.empty((rows, vocab), dtype=torch.bfloat16, device=device)
+                       if store_logits else None)
         self.workspace = None
         if d is not None:
             self.backward_workspace(d)
@@ -318,7 +323,7 @@ def linear_cross_entropy_forward(hidden: torch.Tensor, weight: torch.Tensor,
               weight.stride(0), targets.data_ptr(), rows, vocab, d, state.part_max.data_ptr(),
               state.part_sum.data_ptr(), state.target_logit.data_ptr(), state.lse.data_ptr(),
               state.loss.data_ptr(), state.mean.data_ptr(), state.count.data_ptr(),
-              _hip.stream(hidden))
+              _hip.ptr(state.logits), _hip.stream(hidden))
     return state
 
 
@@ -351,7 +356,8 @@ def linear_cross_entropy_backward(hidden: torch.Tensor, weight: torch.Tensor,
               grad_mean.data_ptr(), rows, vocab, d, workspace.data_ptr(), state.chunk_rows,
               out.data_ptr(), out.stride(0),
               None if weight_grad is None else weight_grad.data_ptr(),
-              0 if weight_grad is None else weight_grad.stride(0), _hip.stream(hidden))
+              0 if weight_grad is None else weight_grad.stride(0), _hip.ptr(state.logits),
+              _hip.stream(hidden))
     return out
 
 
