@@ -265,30 +265,33 @@ def bench_extra(args, device):
     del x, w
     c5 = lm_head_inputs(seed=0)
     hidden, weight, targets = (c5[k].to(device) for k in ("hidden", "weight", "targets"))
-    state = CrossEntropyState(M, VOCAB, device)
     dh = torch.empty((M, D), dtype=torch.bfloat16, device=device)
     one = torch.ones((), device=device)
-
-    def ce():
-        linear_cross_entropy_forward(hidden, weight, targets, state)
-        linear_cross_entropy_backward(hidden, weight, targets, state, one, out=dh)
-
-    for _ in range(args.warmup):
-        ce()
-    t = Timer()
-    for _ in range(args.steps):
-        with t.region("fwd"):
-            linear_cross_entropy_forward(hidden, weight, targets, state)
-        with t.region("bwd"):
-            linear_cross_entropy_backward(hidden, weight, targets, state, one, out=dh)
-    torch.cuda.synchronize()
     f5 = 4 * M * D * VOCAB
-    ms = t.mean_ms("fwd") + t.mean_ms("bwd")
-    res["config5_lm_head_ce_16384x2048x32768"] = {
-        "ms": round(ms, 4), "fwd_ms": round(t.mean_ms("fwd"), 4),
-        "bwd_ms": round(t.mean_ms("bwd"), 4), "tflops": round(f5 / ms / 1e9, 1),
-        "pct_peak": round(100 * f5 / ms / 1e9 / PEAK_BF16_TFLOPS, 2),
-        "flops_note": "logits fwd + dHidden; the backward's logit recompute is not counted"}
+    # Two variants: logits only in registers (the backward recomputes them with a GEMM),
+    # and logits stored by the forward (1 GiB of BF16) and read by the backward.
+    for key, store, note in (
+            ("config5_lm_head_ce_16384x2048x32768", False,
+             "logits fwd + dHidden; the backward's logit recompute is not counted"),
+            ("config5_lm_head_ce_stored_logits_16384x2048x32768", True,
+             "logits fwd + dHidden; the forward stores the BF16 logits, the backward reads them")):
+        state = CrossEntropyState(M, VOCAB, device, store_logits=store)
+        for _ in range(args.warmup):
+            linear_cross_entropy_forward(hidden, weight, targets, state)
+            linear_cross_entropy_backward(hidden, weight, targets, state, one, out=dh)
+        t = Timer()
+        for _ in range(args.steps):
+            with t.region("fwd"):
+                linear_cross_entropy_forward(hidden, weight, targets, state)
+            with t.region("bwd"):
+                linear_cross_entropy_backward(hidden, weight, targets, state, one, out=dh)
+        torch.cuda.synchronize()
+        ms = t.mean_ms("fwd") + t.mean_ms("bwd")
+        res[key] = {
+            "ms": round(ms, 4), "fwd_ms": round(t.mean_ms("fwd"), 4),
+            "bwd_ms": round(t.mean_ms("bwd"), 4), "tflops": round(f5 / ms / 1e9, 1),
+            "pct_peak": round(100 * f5 / ms / 1e9 / PEAK_BF16_TFLOPS, 2), "flops_note": note}
+        del state
     return res
 
 
