@@ -17,7 +17,8 @@ HBM:
 ``value`` is the step's algorithmic FLOPs over its wall time (TFLOP/s). The other two
 configurations are timed beside it and reported under ``per_config``: config 1 (SwiGLU
 4096 x 1024 -> 2 x 2816) and config 5 (LM head with fused cross-entropy, forward
-statistics + dHidden, 16384 x 2048 -> 32768, logits never in HBM).
+statistics + dHidden, 16384 x 2048 -> 32768, once with the logits only in registers and
+once with the forward storing them for the backward).
 
 ``roofline`` describes the dominant kernel of the step (the FP32-accumulating wgrad GEMM
 of the MLP backward by default); its average launch time comes from HIP events around
