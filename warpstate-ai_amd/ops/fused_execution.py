@@ -24,7 +24,11 @@ import torch
 
 from ops import _hip
 
-DEFAULT_CE_CHUNK_ROWS = 4096
+# Rows per LM-head backward chunk. At d = 2048 one 8192-row chunk's dHidden GEMM is 256
+# tiles, one full round on 256 CUs without a vocabulary split; its BF16 logit gradients
+# take 512 MiB at vocab 32768 (config 5: 5 % faster than 4096-row chunks, both with and
+# without stored logits).
+DEFAULT_CE_CHUNK_ROWS = 8192
 
 
 def _check_bf16_cuda(*tensors):
