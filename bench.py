@@ -213,6 +213,20 @@ def bench_gpu(args):
     rstd_bytes = m * D * 2 + m * 4
     hbm = {"rms_rstd": {"ms": round(rstd_ms, 4), "bytes": rstd_bytes,
                         "gbs": round(rstd_bytes / rstd_ms / 1e6, 1)}}
+    # RMSNorm backward of the step (dX and the weight gradient, both launches): x and the
+    # incoming gradient read, dX written, rstd read and the FP32 weight gradient written
+    # once each (the per-block partials are not counted).
+    from ops.activation_execution import _rms_backward
+
+    for _ in range(args.steps):
+        with rt.region("rms_bwd"):
+            _rms_backward(inp["qkv_x"], inp["qkv_norm_weight"], out["rstd"], out["qkv_z"], True)
+    torch.cuda.synchronize()
+    bwd_ms = rt.mean_ms("rms_bwd")
+    bwd_bytes = 3 * m * D * 2 + m * 4 + D * 4
+    hbm["rmsnorm_backward"] = {"ms": round(bwd_ms, 4), "bytes": bwd_bytes,
+                               "gbs": round(bwd_bytes / bwd_ms / 1e6, 1),
+                               "frac_hbm": round(bwd_bytes / bwd_ms / 1e6 / PEAK_HBM_GBS, 4)}
     return wall_ms, sum(flops.values()), regions, kernels, hbm, inp, out
 
 
