@@ -114,3 +114,21 @@ def test_grouped_workspace_query():
     assert q(rows((2048, 2048), (2048, 2048)), 2, 16384) >= 2 * 2048 * 2048
     need = q(rows((2048, 5632), (11264, 2048)), 2, 16384)
     assert need > 0 and need % 65536 == 0
+
+
+def test_grouped_fallback_splits_follow_auto_splits():
+    """A group with fewer tiles than compute units falls back to one call per gradient,
+    each split by the library's port of ops.fused_execution.auto_splits: the group's
+    workspace is the largest of those single calls' workspaces."""
+    from ops.fused_execution import auto_splits
+
+    cus = 256  # the query's device count on a host without a GPU
+    for k in (512, 4096, 16384):
+        for shapes in ([(2048, 5632)], [(300, 264), (520, 130)], [(1024, 1024), (4096, 512)]):
+            rows = _hip.problem_table([(1 << 20, 8, 1, 1 << 20, 8, 1, 1 << 20, n, m, n)
+                                       for m, n in shapes])
+            tiles = sum(-(-m // 256) * -(-n // 256) for m, n in shapes)
+            assert tiles < cus
+            want = max(_hip.query("ws_mm_accumulate_workspace_floats", m, n, k,
+                                  auto_splits(m, n, k, cus)) for m, n in shapes)
+            assert _hip.query("ws_mm_accumulate_group_workspace_floats", rows, len(shapes), k) == want
