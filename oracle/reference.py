@@ -155,18 +155,6 @@ def linear_cross_entropy(hidden, weight, targets, chunk: int = 1024):
     return torch.cat(losses), mean.detach(), int(targets.ne(-100).sum()), dhidden
 
 
-def linear_cross_entropy_loss_only(hidden, weight, targets, chunk: int = 1024):
-    """Per-token loss and mean without the backward (for large CPU baselines)."""
-    losses = []
-    with torch.no_grad():
-        for start in range(0, hidden.shape[0], chunk):
-            logits = F.linear(hidden[start:start + chunk], weight).float()
-            losses.append(F.cross_entropy(logits, targets[start:start + chunk],
-                                          ignore_index=-100, reduction="none"))
-    loss = torch.cat(losses)
-    return loss, loss.sum() / targets.ne(-100).sum().clamp_min(1)
-
-
 def linear_cross_entropy_weight_grad(hidden, weight, targets, chunk: int = 1024,
                                      grad_mean: float = 1.0):
     """FP32 gradient of the mean tied-head loss with respect to the head weight

@@ -75,13 +75,15 @@ def test_config4_mlp_backward_full():
     x, wug, wd, dy = (inp[k].cuda() for k in ("x", "w_upgate", "w_down", "dy"))
     g_up, g_down = inp["g_upgate"].cuda(), inp["g_down"].cuda()
     packed, act = launch_swiglu_mm(x, wug.T, "tiled", (128, 128, 32, 8, 3), True)
-    dx = mlp_backward(x, wug, wd, packed, act, dy, g_up, g_down)
+    dpacked = torch.empty_like(packed)
+    dx = mlp_backward(x, wug, wd, packed, act, dy, g_up, g_down, dpacked=dpacked)
     torch.cuda.synchronize()
     # The oracle consumes the same saved forward tensors (they are parity-checked in the
     # forward tests), so the backward is compared on identical inputs.
     want_dx, want_dpacked, want_up, want_down = oracle.mlp_backward(
         inp["x"], inp["w_upgate"], inp["w_down"], packed.cpu(), act.cpu(), inp["dy"],
         inp["g_upgate"], inp["g_down"])
+    assert_bf16_close(dpacked, want_dpacked, "config4 dPacked")
     assert_bf16_close(dx, want_dx, "config4 dX")
     assert_f32_close(g_up.cpu(), want_up, "config4 G_upgate")
     assert_f32_close(g_down.cpu(), want_down, "config4 G_down")

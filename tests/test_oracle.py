@@ -70,6 +70,30 @@ def test_mm_exact_on_integer_operands_and_transposes():
     assert torch.equal(oracle.mm(b.T, a.T), exact.T)
 
 
+def test_mm_f32_reference_matches_exact_products_rounded_once():
+    """r(f32(a) @ f32(b)) against the fixture's exact float64 products rounded once: the
+    FP32 sum differs from the exact one by far less than half a BF16 ulp, so at most one
+    ulp on a small fraction of ties."""
+    out = oracle.mm_f32_reference(t16("mm_a"), t16("mm_b"))
+    assert out.dtype == torch.bfloat16
+    assert_bf16_bits_close(out, FIX["mm_c"], max_frac=0.01)
+
+
+def test_mm_f32_reference_exact_on_integer_operands_and_order():
+    gen = torch.Generator().manual_seed(6)
+    a = torch.randint(-4, 5, (19, 67), generator=gen).bfloat16()
+    b = torch.randint(-4, 5, (67, 23), generator=gen).bfloat16()
+    exact = (a.double() @ b.double()).bfloat16()
+    assert torch.equal(oracle.mm_f32_reference(a, b), exact)
+    assert torch.equal(oracle.mm_f32_reference(b.T, a.T), exact.T)
+    # A sum whose exact value needs more than BF16's 8 bits is rounded once at the end:
+    # 257 = 256 + 1 rounds to 256 (ties to even), while per-term BF16 rounding would not
+    # change it; 255 + 2 = 257 -> 256 and 256 + 3 = 259 -> 260.
+    a2 = torch.tensor([[255.0, 2.0], [256.0, 3.0]]).bfloat16()
+    b2 = torch.tensor([[1.0], [1.0]]).bfloat16()
+    assert oracle.mm_f32_reference(a2, b2).float().flatten().tolist() == [256.0, 260.0]
+
+
 # --- Paired SwiGLU GEMM --------------------------------------------------------------
 
 @pytest.mark.parametrize("eager", [True, False])

@@ -118,13 +118,40 @@ def _rms_autograd(ctx, grad, _grad_rstd):
 bf16_rmsnorm.register_autograd(_rms_autograd, setup_context=_rms_setup)
 
 
+_MODES = {"baseline": (), "swiglu": ("swiglu",), "rmsnorm": ("rmsnorm",),
+          "all": ("swiglu", "rmsnorm")}
+
+
+def _fused_swiglu_forward(module, x, _original):
+    """up_gate, then the SwiGLU row kernel on the packed projection, then down."""
+    act = bf16_swiglu(module.up_gate(x).contiguous(),
+                      eager_rounding=not torch.compiler.is_compiling())
+    return module.down(act)
+
+
+def _rms_input_ok(module, x) -> bool:
+    """Training calls the RMSNorm row kernels take: a non-empty contiguous BF16 CUDA tensor
+    whose rows fit the kernels (at most 8192 features)."""
+    return (module.training and torch.is_grad_enabled() and x.is_cuda
+            and x.dtype == torch.bfloat16 and x.is_contiguous() and x.numel() > 0
+            and 0 < x.shape[-1] <= 8192)
+
+
+def _fused_rms_forward(module, x, _original):
+    return bf16_rmsnorm(x, module.weight, module.eps,
+                        eager_rounding=not torch.compiler.is_compiling())[0]
+
+
 def apply_activation_execution(model: torch.nn.Module, mode: str = "baseline") -> None:
-    """Patch training forwards only, keeping the canonical FP32 parameter objects
-    (ops/activation_execution.py:212-253). Modes: ``swiglu``, ``rmsnorm``, ``all``;
-    ``baseline`` is a no-op. Unsupported inputs and evaluation use the original forward."""
+    """Send the SwiGLU and/or RMSNorm modules' training forwards to the HIP row kernels
+    (ops/activation_execution.py:212-253); ``baseline`` changes nothing. The FP32 parameter
+    objects and the state dict stay as they are, and other calls keep the original path.
+    Eager calls keep eager BF16 rounding; traced calls use the compiled arithmetic."""
     from warpstate.model import RMSNorm, SwiGLU
 
-    if mode not in {"baseline", "swiglu", "rmsnorm", "all"}:
+    from ops._patching import bf16_autocast_training, install_forward
+
+    if mode not in _MODES:
         raise ValueError(f"Unknown activation execution mode: {mode}")
     if getattr(model, "_activation_execution_mode", "baseline") != "baseline":
         raise ValueError("Activation execution has already been applied")
@@ -132,26 +159,12 @@ def apply_activation_execution(model: torch.nn.Module, mode: str = "baseline") -
         return
     if any(p.dtype != torch.float32 for p in model.parameters()):
         raise ValueError("Activation execution requires FP32 master parameters")
-
+    routes = {"swiglu": (SwiGLU, _fused_swiglu_forward, bf16_autocast_training),
+              "rmsnorm": (RMSNorm, _fused_rms_forward, _rms_input_ok)}
+    selected = [routes[name] for name in _MODES[mode]]
     for module in model.modules():
-        original = module.forward
-        if isinstance(module, SwiGLU) and mode in {"swiglu", "all"}:
-            def swiglu_forward(x, _module=module, _original=original):
-                if (_module.training and torch.is_grad_enabled() and x.is_cuda
-                        and torch.is_autocast_enabled("cuda")
-                        and torch.get_autocast_dtype("cuda") == torch.bfloat16):
-                    packed = _module.up_gate(x)
-                    return _module.down(bf16_swiglu(
-                        packed.contiguous(), eager_rounding=not torch.compiler.is_compiling()))
-                return _original(x)
-            module.forward = swiglu_forward
-        elif isinstance(module, RMSNorm) and mode in {"rmsnorm", "all"}:
-            def rms_forward(x, _module=module, _original=original):
-                if (_module.training and torch.is_grad_enabled() and x.is_cuda
-                        and x.dtype == torch.bfloat16 and x.is_contiguous()
-                        and 0 < x.shape[-1] <= 8192 and x.numel() > 0):
-                    return bf16_rmsnorm(x, _module.weight, _module.eps,
-                                        eager_rounding=not torch.compiler.is_compiling())[0]
-                return _original(x)
-            module.forward = rms_forward
+        for kind, body, eligible in selected:
+            if isinstance(module, kind):
+                install_forward(module, body, eligible)
+                break
     model._activation_execution_mode = mode

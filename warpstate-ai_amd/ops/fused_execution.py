@@ -393,16 +393,18 @@ def linear_cross_entropy(hidden, weight, targets):
 def mlp_backward(x: torch.Tensor, w_upgate: torch.Tensor, w_down: torch.Tensor,
                  packed: torch.Tensor, act: torch.Tensor, dy: torch.Tensor,
                  g_upgate: torch.Tensor, g_down: torch.Tensor, eager_rounding: bool = True,
-                 dw_splits: int | None = None) -> torch.Tensor:
+                 dw_splits: int | None = None,
+                 dpacked: torch.Tensor | None = None) -> torch.Tensor:
     """Backward of y = down(silu(gate) * up) with (up | gate) = x @ w_upgate.T.
 
     x [M, d], w_upgate [2H, d], w_down [d, H] (nn.Linear layouts, BF16), packed [M, 2H] and
     act [M, H] saved from the forward, dy [M, d]. Accumulates G_down [d, H] += f32(r(dY^T act))
     and G_upgate [2H, d] += f32(r(dPacked^T x)); returns dX [M, d]. Restates
     ops/matmul_execution.py:236-244 and :314-319 with the SwiGLU backward fused on the
-    dAct GEMM.
+    dAct GEMM. ``dpacked`` (contiguous BF16 [M, 2H]), when given, receives the gradient of
+    the packed projection.
     """
-    dpacked = swiglu_backward_mm(dy, w_down, packed, eager_rounding)
+    dpacked = swiglu_backward_mm(dy, w_down, packed, eager_rounding, out=dpacked)
     dx = mm(dpacked, w_upgate)
     if dw_splits is None:
         # Both weight gradients reduce over the tokens: one launch fills the GPU with them.

@@ -1,18 +1,28 @@
-"""Opt-in, shape-specific BF16 matrix execution with ordinary autograd ownership, on gfx950.
+"""Plan-selected BF16 GEMMs behind registered operators, for gfx950.
 
-Call surface of WarpState's ``ops/matmul_execution.py``: the strict JSON plan
-(``warpstate-matmul-plan-v1``), exact (kind, m, n, k, strides) selection, the registered
-operators ``warpstate::{selected_matrix_kernel, planned_mm, selected_swiglu_kernel,
-selected_swiglu_gradient_kernel, planned_swiglu_mm}`` with their autograd and fake
-implementations, and model patching. Plans are validated and registered once, before
-compiling cores or constructing DDP. Selected shapes launch the HIP kernels of
-``libwarpstate_hip.so``; unselected shapes use ATen. CPU and evaluation paths stay
-original; FP32 parameter casts stay inside each visible forward graph.
+Interface (kept so that plans, compiled graphs and callers written for WarpState's
+``ops/matmul_execution.py`` work unchanged): the ``warpstate-matmul-plan-v1`` document and
+its validation messages, ``MatmulEntry`` / ``MatmulPlan``, ``matmul_plan_from_dict``,
+``load_matmul_plan``, ``planned_matmul``, ``apply_matmul_execution``, and the operators
+``warpstate::{selected_matrix_kernel, planned_mm, selected_swiglu_kernel,
+selected_swiglu_gradient_kernel, planned_swiglu_mm}`` with their schemas, fake tensors and
+autograd formulas.
+
+How it works here:
+* A plan is parsed once into immutable entries plus a dictionary from the exact
+  (kind, m, n, k, a strides, b strides) key to its entry, so selection during a forward is
+  one lookup. Plans are registered in a process-wide table under a key that covers the
+  plan's canonical JSON and the SHA-256 of the sources that execute it (Python and HIP).
+* The operators decide on the host, before any launch, whether a call is served by a HIP
+  kernel of ``libwarpstate_hip.so`` or by ATen (no entry, an ``aten`` entry, CPU operands,
+  or operands that lost the alignment an aligned-load entry needs).
+* The weight-gradient GEMM of every projection is issued as dY^T @ X, the nn.Linear dW
+  orientation the tuner measures, and its transpose is returned as the gradient of B = W^T.
 """
 
 from __future__ import annotations
 
-from dataclasses import dataclass
+from dataclasses import dataclass, field
 import hashlib
 import json
 import os
@@ -21,15 +31,30 @@ from pathlib import Path
 import torch
 from torch.library import custom_op
 
+from ops._patching import install_forward
+
 PLAN_FORMAT = "warpstate-matmul-plan-v1"
-_DEFAULT_TILE = (64, 64, 32, 4, 3)
 _TILE_FIELDS = ("block_m", "block_n", "block_k", "num_warps", "num_stages")
-_PLANS: dict[str, "MatmulPlan"] = {}
+_DEFAULT_TILE = (64, 64, 32, 4, 3)
+_KINDS = ("mm", "swiglu")
+_ALGORITHMS = ("aten", "tiled", "persistent", "persistent_tma")
+_DOCUMENT_FIELDS = frozenset({"format", "description", "entries"})
+_ENTRY_FIELDS = frozenset({"kind", "m", "n", "k", "a_stride", "b_stride", "dtype",
+                           "algorithm", "tile", "name"})
 _PACKAGE = Path(__file__).resolve().parents[1]
+# Sources whose bytes are part of a plan's identity: the Python that selects and launches
+# and the HIP that computes. Fused SwiGLU plans add the epilogue's modules.
+_SOURCES = ("ops/matmul_execution.py", "ops/matmul_kernels.py", "csrc/gemm.h",
+            "csrc/gemm_fast.h", "csrc/mm.hip")
+_SWIGLU_SOURCES = ("ops/matmul_epilogue.py", "ops/activation_execution.py", "csrc/rowops.h")
+
+_PLANS: dict[str, "MatmulPlan"] = {}
 
 
 @dataclass(frozen=True)
 class MatmulEntry:
+    """One selected shape/layout: operation kind, sizes, element strides of A [m, k] and
+    B [k, n], the algorithm and its five-field tile."""
     kind: str
     m: int
     n: int
@@ -41,10 +66,10 @@ class MatmulEntry:
     name: str = ""
 
     @property
-    def key(self):
+    def key(self) -> tuple:
         return (self.kind, self.m, self.n, self.k, *self.a_stride, *self.b_stride)
 
-    def as_dict(self):
+    def as_dict(self) -> dict:
         return {"kind": self.kind, "m": self.m, "n": self.n, "k": self.k,
                 "a_stride": list(self.a_stride), "b_stride": list(self.b_stride),
                 "dtype": "bfloat16", "algorithm": self.algorithm,
@@ -53,351 +78,389 @@ class MatmulEntry:
 
 @dataclass(frozen=True)
 class MatmulPlan:
+    """A validated plan: entries in document order, the canonical digest, the source
+    digests and the registry key. ``select`` reads a prebuilt index only."""
     entries: tuple[MatmulEntry, ...]
     sha256: str
     source_hashes: tuple[tuple[str, str], ...]
     registry_key: str
     description: str = ""
+    _index: dict = field(init=False, repr=False, compare=False, hash=False)
+
+    def __post_init__(self):
+        object.__setattr__(self, "_index", {entry.key: entry for entry in self.entries})
 
     @property
-    def metadata(self):
-        """Serializable provenance for runtime records and resume signatures."""
+    def metadata(self) -> dict:
+        """The plan's provenance as plain JSON values (for run records and resume
+        signatures)."""
         return {"format": PLAN_FORMAT, "sha256": self.sha256,
                 "source_sha256": dict(self.source_hashes),
                 "entries": [entry.as_dict() for entry in self.entries]}
 
-    def select(self, kind, m, n, k, a_stride, b_stride):
-        """Pure shape/layout lookup; no device work or filesystem access."""
-        wanted = (kind, m, n, k, *a_stride, *b_stride)
-        return next((entry for entry in self.entries if entry.key == wanted), None)
+    def select(self, kind, m, n, k, a_stride, b_stride) -> MatmulEntry | None:
+        return self._index.get((kind, m, n, k, *a_stride, *b_stride))
 
 
-def _positive_integer(value, name):
-    if isinstance(value, bool) or not isinstance(value, int) or value < 1:
-        raise ValueError(f"{name} must be a positive integer")
+# --- reading a plan document ------------------------------------------------------------
+
+def _require(condition: bool, message: str) -> None:
+    if not condition:
+        raise ValueError(message)
+
+
+def _count(value, name: str) -> int:
+    """A positive int (bool is not accepted as an int)."""
+    _require(type(value) is int and value >= 1, f"{name} must be a positive integer")
     return value
 
 
-def _stride(value, name):
-    if not isinstance(value, list) or len(value) != 2:
-        raise ValueError(f"{name} must contain two positive integer strides")
-    return tuple(_positive_integer(item, name) for item in value)
+def _strides(value, name: str) -> tuple[int, int]:
+    _require(isinstance(value, list) and len(value) == 2,
+             f"{name} must contain two positive integer strides")
+    return (_count(value[0], name), _count(value[1], name))
 
 
-def _no_duplicate_json_keys(pairs):
-    document = {}
-    for key, value in pairs:
-        if key in document:
-            raise ValueError(f"Duplicate JSON key: {key}")
-        document[key] = value
-    return document
+def _tile(row: dict, kind: str) -> tuple[int, int, int, int, int]:
+    from ops.matmul_kernels import normalize_tile
+
+    document = row.get("tile")
+    if document is None and "tile" not in row:
+        return normalize_tile(dict(zip(_TILE_FIELDS, _DEFAULT_TILE)))
+    _require(isinstance(document, dict) and set(document) == set(_TILE_FIELDS),
+             "Matmul tile must specify block_m/block_n/block_k/num_warps/num_stages")
+    for name in _TILE_FIELDS:
+        _count(document[name], name)
+    tile = normalize_tile(document)
+    if kind == "swiglu":
+        # block_n counts one half of the pair: A plus two B panels per stage.
+        bm, bn, bk, _warps, stages = tile
+        _require((bm + 2 * bn) * bk * 2 * stages <= 96 * 1024,
+                 "Fused SwiGLU tile exceeds the conservative shared-memory budget")
+    return tile
 
 
-def _implementation_hashes(has_fused_swiglu):
-    """SHA-256 of this implementation's own sources, keyed like the reference's files.
+def _entry(index: int, row) -> MatmulEntry:
+    _require(isinstance(row, dict) and set(row) <= _ENTRY_FIELDS,
+             f"Unknown fields in matmul entry {index}")
+    kind, algorithm = row.get("kind"), row.get("algorithm")
+    _require(kind in _KINDS, "Matmul entry kind must be mm or swiglu")
+    _require(row.get("dtype") == "bfloat16", "Matmul plans support BF16 operands only")
+    _require(algorithm in _ALGORITHMS, "Unknown matmul algorithm")
+    _require(not (kind == "swiglu" and algorithm == "persistent_tma"),
+             "Fused SwiGLU does not yet support the persistent_tma algorithm")
+    m, n, k = (_count(row.get(name), name) for name in ("m", "n", "k"))
+    _require(kind != "swiglu" or n % 2 == 0, "Fused SwiGLU output width must be even")
+    name = row.get("name", "")
+    _require(isinstance(name, str), "Matmul entry name must be a string")
+    tile = _tile(row, kind)
+    return MatmulEntry(kind, m, n, k, _strides(row.get("a_stride"), "a_stride"),
+                       _strides(row.get("b_stride"), "b_stride"), algorithm, tile, name)
 
-    The HIP sources behind the kernels are part of the provenance, so a kernel change
-    changes the execution signature just as a Triton source change does in the reference
-    (ops/matmul_execution.py:96-102).
-    """
-    names = {"ops/matmul_execution.py": _PACKAGE / "ops" / "matmul_execution.py",
-             "ops/matmul_kernels.py": _PACKAGE / "ops" / "matmul_kernels.py",
-             "csrc/gemm.h": _PACKAGE / "csrc" / "gemm.h",
-             "csrc/mm.hip": _PACKAGE / "csrc" / "mm.hip"}
-    if has_fused_swiglu:
-        names["ops/matmul_epilogue.py"] = _PACKAGE / "ops" / "matmul_epilogue.py"
-        names["ops/activation_execution.py"] = _PACKAGE / "ops" / "activation_execution.py"
-        names["csrc/rowops.h"] = _PACKAGE / "csrc" / "rowops.h"
-    return tuple((name, hashlib.sha256(path.read_bytes()).hexdigest())
-                 for name, path in sorted(names.items()))
+
+def _digest(text: str) -> str:
+    return hashlib.sha256(text.encode()).hexdigest()
+
+
+def _source_hashes(with_swiglu: bool) -> tuple[tuple[str, str], ...]:
+    names = _SOURCES + (_SWIGLU_SOURCES if with_swiglu else ())
+    return tuple((name, hashlib.sha256((_PACKAGE / name).read_bytes()).hexdigest())
+                 for name in sorted(names))
 
 
 def matmul_plan_from_dict(document: dict) -> MatmulPlan:
-    """Validate a source recipe; later selection only uses immutable data
-    (ops/matmul_execution.py:105-169)."""
-    from ops.matmul_kernels import normalize_tile
+    """Validate a plan document and register it (ops/matmul_execution.py:105-169).
 
-    if not isinstance(document, dict):
-        raise ValueError("Matmul plan must be a JSON object")
-    if set(document) - {"format", "description", "entries"}:
-        raise ValueError("Unknown matmul plan fields")
-    if document.get("format") != PLAN_FORMAT:
-        raise ValueError(f"Matmul plan format must be {PLAN_FORMAT}")
+    Errors are ``ValueError`` with the reference's messages, raised in its order: document
+    shape, format, description, entries; then per entry its fields, kind, dtype,
+    algorithm, sizes, name, tile and strides; then duplicate keys."""
+    _require(isinstance(document, dict), "Matmul plan must be a JSON object")
+    _require(set(document) <= _DOCUMENT_FIELDS, "Unknown matmul plan fields")
+    _require(document.get("format") == PLAN_FORMAT, f"Matmul plan format must be {PLAN_FORMAT}")
     description = document.get("description", "")
-    if not isinstance(description, str):
-        raise ValueError("Matmul plan description must be a string")
-    if not isinstance(document.get("entries"), list):
-        raise ValueError("Matmul plan entries must be a list")
-    allowed = {"kind", "m", "n", "k", "a_stride", "b_stride", "dtype", "algorithm", "tile", "name"}
-    entries, seen = [], set()
-    for index, row in enumerate(document["entries"]):
-        if not isinstance(row, dict) or set(row) - allowed:
-            raise ValueError(f"Unknown fields in matmul entry {index}")
-        if row.get("kind") not in {"mm", "swiglu"}:
-            raise ValueError("Matmul entry kind must be mm or swiglu")
-        if row.get("dtype") != "bfloat16":
-            raise ValueError("Matmul plans support BF16 operands only")
-        if row.get("algorithm") not in {"aten", "tiled", "persistent", "persistent_tma"}:
-            raise ValueError("Unknown matmul algorithm")
-        if row["kind"] == "swiglu" and row["algorithm"] == "persistent_tma":
-            raise ValueError("Fused SwiGLU does not yet support the persistent_tma algorithm")
-        dimensions = tuple(_positive_integer(row.get(name), name) for name in ("m", "n", "k"))
-        if row["kind"] == "swiglu" and dimensions[1] % 2:
-            raise ValueError("Fused SwiGLU output width must be even")
-        name = row.get("name", "")
-        if not isinstance(name, str):
-            raise ValueError("Matmul entry name must be a string")
-        tile_document = row.get("tile", dict(zip(_TILE_FIELDS, _DEFAULT_TILE, strict=True)))
-        if not isinstance(tile_document, dict) or set(tile_document) != set(_TILE_FIELDS):
-            raise ValueError("Matmul tile must specify block_m/block_n/block_k/num_warps/num_stages")
-        for field, value in tile_document.items():
-            _positive_integer(value, field)
-        tile = tuple(normalize_tile(tile_document))
-        if row["kind"] == "swiglu":
-            block_m, block_n, block_k, _warps, stages = tile
-            if (block_m + 2 * block_n) * block_k * 2 * stages > 96 * 1024:
-                raise ValueError("Fused SwiGLU tile exceeds the conservative shared-memory budget")
-        entry = MatmulEntry(row["kind"], *dimensions,
-                            _stride(row.get("a_stride"), "a_stride"),
-                            _stride(row.get("b_stride"), "b_stride"),
-                            row["algorithm"], tile, name)
-        if entry.key in seen:
-            raise ValueError("Duplicate matmul shape/layout entry")
-        seen.add(entry.key)
+    _require(isinstance(description, str), "Matmul plan description must be a string")
+    rows = document.get("entries")
+    _require(isinstance(rows, list), "Matmul plan entries must be a list")
+    entries: list[MatmulEntry] = []
+    keys: set[tuple] = set()
+    for index, row in enumerate(rows):
+        entry = _entry(index, row)
+        _require(entry.key not in keys, "Duplicate matmul shape/layout entry")
+        keys.add(entry.key)
         entries.append(entry)
-    canonical = {"format": PLAN_FORMAT, "description": description,
-                 "entries": [entry.as_dict() for entry in entries]}
-    digest = hashlib.sha256(
-        json.dumps(canonical, sort_keys=True, separators=(",", ":")).encode()).hexdigest()
-    hashes = _implementation_hashes(any(entry.kind == "swiglu" for entry in entries))
-    registry_key = hashlib.sha256((digest + json.dumps(hashes)).encode()).hexdigest()
-    plan = MatmulPlan(tuple(entries), digest, hashes, registry_key, description)
-    existing = _PLANS.get(registry_key)
-    if existing is not None and existing != plan:
+    canonical = json.dumps({"format": PLAN_FORMAT, "description": description,
+                            "entries": [entry.as_dict() for entry in entries]},
+                           sort_keys=True, separators=(",", ":"))
+    sha = _digest(canonical)
+    sources = _source_hashes(any(entry.kind == "swiglu" for entry in entries))
+    plan = MatmulPlan(tuple(entries), sha, sources, _digest(sha + json.dumps(sources)),
+                      description)
+    registered = _PLANS.setdefault(plan.registry_key, plan)
+    if registered != plan:
         raise RuntimeError("Matmul plan registry identity collision")
-    _PLANS[registry_key] = plan
     return plan
 
 
 def _workspace() -> Path:
-    """Directory plans must live under: $WARPSTATE_WORKSPACE, else this checkout's parent."""
+    """Root under which plan files must live: $WARPSTATE_WORKSPACE when set, otherwise the
+    directory that holds this checkout."""
     configured = os.environ.get("WARPSTATE_WORKSPACE")
     return Path(configured).expanduser().resolve() if configured else _PACKAGE.parents[1]
 
 
+def _reject_duplicate_keys(pairs: list) -> dict:
+    document: dict = {}
+    for key, value in pairs:
+        _require(key not in document, f"Duplicate JSON key: {key}")
+        document[key] = value
+    return document
+
+
 def load_matmul_plan(path: str | Path) -> MatmulPlan:
-    """Load once before training; no recipes or hashes are read during forward."""
+    """Read, validate and register a plan file; call before compiling or training, since
+    forwards only consult registered plans."""
     path = Path(path).expanduser().resolve()
-    if not path.is_relative_to(_workspace()):
-        raise ValueError("Matmul plan must remain inside the WarpState workspace")
-    document = json.loads(path.read_text(), object_pairs_hook=_no_duplicate_json_keys)
-    return matmul_plan_from_dict(document)
+    _require(path.is_relative_to(_workspace()),
+             "Matmul plan must remain inside the WarpState workspace")
+    return matmul_plan_from_dict(json.loads(path.read_text(),
+                                            object_pairs_hook=_reject_duplicate_keys))
+
+
+# --- selection -------------------------------------------------------------------------
+
+def _launchable(a: torch.Tensor, b: torch.Tensor) -> bool:
+    """Operands a HIP kernel can take at all: two non-empty BF16 CUDA matrices on one
+    device with matching inner sizes and positive strides."""
+    return (a.ndim == 2 and b.ndim == 2 and a.is_cuda and b.is_cuda and a.device == b.device
+            and a.dtype == torch.bfloat16 and b.dtype == torch.bfloat16
+            and a.shape[1] == b.shape[0] and a.numel() > 0 and b.numel() > 0
+            and min(*a.stride(), *b.stride()) > 0)
+
+
+def _aligned_rows(t: torch.Tensor) -> bool:
+    """Unit inner stride, 16-byte row pitch and a 16-byte-aligned storage offset: what the
+    aligned-load (``persistent_tma``) kernels assume. A view sliced out of an aligned
+    allocation can keep its shape and strides and still fail the offset test."""
+    return (min(t.stride()) == 1 and max(t.stride()) * 2 % 16 == 0
+            and t.storage_offset() * 2 % 16 == 0)
 
 
 def _choice(a, b, plan_key, kind="mm"):
-    """Eligible plan entry for these operands, or None (ops/matmul_execution.py:182-198)."""
-    if (a.ndim != 2 or b.ndim != 2 or not a.is_cuda or not b.is_cuda
-            or a.device != b.device or a.dtype != torch.bfloat16
-            or b.dtype != torch.bfloat16 or a.shape[1] != b.shape[0]
-            or a.numel() == 0 or b.numel() == 0
-            or any(stride <= 0 for stride in (*a.stride(), *b.stride()))):
+    """The entry that serves these operands, or None for ATen (ops/matmul_execution.py:182-198)."""
+    if not _launchable(a, b):
         return None
     entry = _PLANS[plan_key].select(kind, a.shape[0], b.shape[1], a.shape[1],
                                     a.stride(), b.stride())
     if entry is not None and entry.algorithm == "persistent_tma":
-        # Sliced views may lose the aligned base that the aligned-operand kernel assumes.
-        if (min(a.stride()) != 1 or min(b.stride()) != 1
-                or max(a.stride()) * 2 % 16 or max(b.stride()) * 2 % 16
-                or a.storage_offset() * 2 % 16 or b.storage_offset() * 2 % 16):
+        if not (_aligned_rows(a) and _aligned_rows(b)):
             return None
     return entry
 
 
+def _served(entry: MatmulEntry | None) -> bool:
+    return entry is not None and entry.algorithm != "aten"
+
+
+# --- registered operators ---------------------------------------------------------------
+
 @custom_op("warpstate::selected_matrix_kernel", mutates_args=())
 def _selected_matrix_kernel(a: torch.Tensor, b: torch.Tensor, plan_key: str) -> torch.Tensor:
-    """Opaque launch, keeping the outer operator's registered autograd."""
+    """The GEMM launch as one opaque node, so that compiled autograd re-traces the outer
+    operator's backward without looking inside the kernel call."""
     from ops.matmul_kernels import launch_mm
 
     entry = _choice(a, b, plan_key)
-    if entry is None or entry.algorithm == "aten":
-        return torch.mm(a, b)
-    return launch_mm(a, b, entry.algorithm, entry.tile)
+    return launch_mm(a, b, entry.algorithm, entry.tile) if _served(entry) else torch.mm(a, b)
 
 
 @_selected_matrix_kernel.register_fake
-def _selected_matrix_kernel_fake(a, b, plan_key):
-    return torch.empty((a.shape[0], b.shape[1]), dtype=a.dtype, device=a.device)
+def _(a, b, plan_key):
+    return a.new_empty((a.shape[0], b.shape[1]))
 
 
 @custom_op("warpstate::planned_mm", mutates_args=())
 def _planned_mm(a: torch.Tensor, b: torch.Tensor, plan_key: str) -> torch.Tensor:
-    entry = _choice(a, b, plan_key)
-    if entry is None or entry.algorithm == "aten":
-        return torch.mm(a, b)
-    return _selected_matrix_kernel(a, b, plan_key)
+    """r(a @ b): selected shapes through the opaque kernel node, the rest through ATen."""
+    if _served(_choice(a, b, plan_key)):
+        return _selected_matrix_kernel(a, b, plan_key)
+    return torch.mm(a, b)
 
 
 @_planned_mm.register_fake
-def _planned_mm_fake(a, b, plan_key):
-    return torch.empty((a.shape[0], b.shape[1]), dtype=a.dtype, device=a.device)
+def _(a, b, plan_key):
+    return a.new_empty((a.shape[0], b.shape[1]))
 
 
-def _mm_setup(ctx, inputs, output):
-    ctx.save_for_backward(inputs[0], inputs[1])
-    ctx.plan_key = inputs[2]
+def _save_operands(ctx, inputs, output):
+    a, b, ctx.plan_key = inputs
+    ctx.save_for_backward(a, b)
+
+
+def _operand_grads(ctx, grad_out, a, b, plan_key):
+    """(dA, dB) of C = A @ B: dA = G B^T, and dB from the dW-oriented product G^T A,
+    transposed back (ops/matmul_execution.py:236-244)."""
+    da = _planned_mm(grad_out, b.T, plan_key) if ctx.needs_input_grad[0] else None
+    db = _planned_mm(grad_out.T, a, plan_key).T if ctx.needs_input_grad[1] else None
+    return da, db
 
 
 def _mm_backward(ctx, grad):
-    """dA = g @ b^T and dB = (g^T @ a)^T, in Linear's dW orientation
-    (ops/matmul_execution.py:236-244)."""
     a, b = ctx.saved_tensors
-    grad = grad.contiguous()
-    da = _planned_mm(grad, b.T, ctx.plan_key) if ctx.needs_input_grad[0] else None
-    db = _planned_mm(grad.T, a, ctx.plan_key).T if ctx.needs_input_grad[1] else None
-    return da, db, None
+    return (*_operand_grads(ctx, grad.contiguous(), a, b, ctx.plan_key), None)
 
 
-_planned_mm.register_autograd(_mm_backward, setup_context=_mm_setup)
+_planned_mm.register_autograd(_mm_backward, setup_context=_save_operands)
 
 
 def planned_matmul(a: torch.Tensor, b: torch.Tensor, plan: MatmulPlan) -> torch.Tensor:
-    """Autograd-enabled entry point, also useful for isolated correctness checks."""
+    """``a @ b`` through ``warpstate::planned_mm`` with autograd."""
     return _planned_mm(a, b, plan.registry_key)
+
+
+def _paired(a, b, entry, eager_rounding):
+    from ops.matmul_epilogue import launch_swiglu_mm
+
+    if _served(entry):
+        return launch_swiglu_mm(a, b, entry.algorithm, entry.tile, eager_rounding)
+    tile = entry.tile if entry is not None else _DEFAULT_TILE
+    return launch_swiglu_mm(a, b, "aten", tile, eager_rounding)
+
+
+def _paired_fake(rows, width, like):
+    return like.new_empty((rows, width)), like.new_empty((rows, width // 2))
 
 
 @custom_op("warpstate::selected_swiglu_kernel", mutates_args=())
 def _selected_swiglu_kernel(a: torch.Tensor, weight: torch.Tensor, plan_key: str,
                             eager_rounding: bool) -> tuple[torch.Tensor, torch.Tensor]:
-    """Takes the native-layout BF16 weight [2H, K]; the projection view B = W^T is formed
-    at launch (ops/matmul_execution.py:255-271)."""
-    from ops.matmul_epilogue import launch_swiglu_mm
-
+    """(packed, act) from the nn.Linear-layout weight [2H, K]: B = W^T is formed inside,
+    so that a compiled graph passes the same BF16 weight here and to the saved-for-backward
+    slot (ops/matmul_execution.py:255-271)."""
     b = weight.T
-    entry = _choice(a, b, plan_key, "swiglu")
-    if entry is None or entry.algorithm == "aten":
-        return launch_swiglu_mm(a, b, "aten", _DEFAULT_TILE, eager_rounding)
-    return launch_swiglu_mm(a, b, entry.algorithm, entry.tile, eager_rounding)
+    return _paired(a, b, _choice(a, b, plan_key, "swiglu"), eager_rounding)
 
 
 @_selected_swiglu_kernel.register_fake
-def _selected_swiglu_kernel_fake(a, weight, plan_key, eager_rounding):
-    packed = torch.empty((a.shape[0], weight.shape[0]), dtype=a.dtype, device=a.device)
-    activation = torch.empty((a.shape[0], weight.shape[0] // 2), dtype=a.dtype, device=a.device)
-    return packed, activation
+def _(a, weight, plan_key, eager_rounding):
+    return _paired_fake(a.shape[0], weight.shape[0], a)
 
 
 @custom_op("warpstate::selected_swiglu_gradient_kernel", mutates_args=())
 def _selected_swiglu_gradient_kernel(packed: torch.Tensor, grad: torch.Tensor,
                                      eager_rounding: bool) -> torch.Tensor:
+    """dUp | dGate of the packed projection (the SwiGLU backward row kernel)."""
     from ops.activation_execution import _swiglu_backward
 
     return _swiglu_backward(packed, grad, eager_rounding)
 
 
 @_selected_swiglu_gradient_kernel.register_fake
-def _selected_swiglu_gradient_kernel_fake(packed, grad, eager_rounding):
+def _(packed, grad, eager_rounding):
     return torch.empty_like(packed)
 
 
 @custom_op("warpstate::planned_swiglu_mm", mutates_args=())
 def _planned_swiglu_mm(a: torch.Tensor, b: torch.Tensor, plan_key: str,
                        eager_rounding: bool) -> tuple[torch.Tensor, torch.Tensor]:
-    from ops.matmul_epilogue import launch_swiglu_mm
-
+    """(packed, act) of the paired projection with the SwiGLU epilogue."""
     entry = _choice(a, b, plan_key, "swiglu")
-    if entry is not None and entry.algorithm != "aten":
+    if _served(entry):
         return _selected_swiglu_kernel(a, b.T, plan_key, eager_rounding)
-    algorithm = entry.algorithm if entry is not None else "aten"
-    tile = entry.tile if entry is not None else _DEFAULT_TILE
-    return launch_swiglu_mm(a, b, algorithm, tile, eager_rounding)
+    return _paired(a, b, entry, eager_rounding)
 
 
 @_planned_swiglu_mm.register_fake
-def _planned_swiglu_mm_fake(a, b, plan_key, eager_rounding):
-    packed = torch.empty((a.shape[0], b.shape[1]), dtype=a.dtype, device=a.device)
-    activation = torch.empty((a.shape[0], b.shape[1] // 2), dtype=a.dtype, device=a.device)
-    return packed, activation
+def _(a, b, plan_key, eager_rounding):
+    return _paired_fake(a.shape[0], b.shape[1], a)
 
 
-def _fused_setup(ctx, inputs, output):
-    ctx.save_for_backward(inputs[0], inputs[1], output[0])
-    ctx.plan_key = inputs[2]
-    ctx.eager_rounding = inputs[3]
-    ctx.mark_non_differentiable(output[0])
+def _save_paired(ctx, inputs, output):
+    a, b, ctx.plan_key, ctx.eager_rounding = inputs
+    packed = output[0]
+    ctx.save_for_backward(a, b, packed)
+    ctx.mark_non_differentiable(packed)
 
 
 def _fused_backward(ctx, _packed_grad, grad):
-    """SwiGLU backward, then dX and dW of the packed projection
+    """Through the activation to dPacked, then dA and dB of the packed projection
     (ops/matmul_execution.py:314-319)."""
     a, b, packed = ctx.saved_tensors
-    projection_grad = _selected_swiglu_gradient_kernel(packed, grad, ctx.eager_rounding)
-    da = _planned_mm(projection_grad, b.T, ctx.plan_key) if ctx.needs_input_grad[0] else None
-    db = _planned_mm(projection_grad.T, a, ctx.plan_key).T if ctx.needs_input_grad[1] else None
-    return da, db, None, None
+    dpacked = _selected_swiglu_gradient_kernel(packed, grad, ctx.eager_rounding)
+    return (*_operand_grads(ctx, dpacked, a, b, ctx.plan_key), None, None)
 
 
-_planned_swiglu_mm.register_autograd(_fused_backward, setup_context=_fused_setup)
+_planned_swiglu_mm.register_autograd(_fused_backward, setup_context=_save_paired)
 
 
-def _linear_has_choices(module, plan):
-    width, output = module.in_features, module.out_features
-    return any(entry.kind == "mm" and (
-        (entry.n == output and entry.k == width)      # forward
-        or (entry.n == width and entry.k == output)   # dX
-        or (entry.m == output and entry.n == width)   # dW
-    ) for entry in plan.entries)
+# --- model patching --------------------------------------------------------------------
+
+def _linear_has_choices(module: torch.nn.Linear, plan: MatmulPlan) -> bool:
+    """Whether any ``mm`` entry can serve one of the Linear's three GEMMs, given as
+    (m, n, k) with None for the token count: the forward [*, in] x [in, out], the input
+    gradient [*, out] x [out, in] and the weight gradient [out, *] x [*, in]."""
+    d_in, d_out = module.in_features, module.out_features
+    gemms = ((None, d_out, d_in), (None, d_in, d_out), (d_out, d_in, None))
+    return any(entry.kind == "mm"
+               and all(want is None or want == got
+                       for want, got in zip(gemm, (entry.m, entry.n, entry.k)))
+               for entry in plan.entries for gemm in gemms)
+
+
+def _rows(x: torch.Tensor) -> torch.Tensor:
+    return x.reshape(-1, x.shape[-1]).to(torch.bfloat16)
+
+
+def _planned_linear(plan_key: str):
+    def run(module, x, _original):
+        out = _planned_mm(_rows(x), module.weight.to(torch.bfloat16).T, plan_key)
+        return out.reshape(*x.shape[:-1], module.out_features)
+    return run
+
+
+def _planned_swiglu(plan_key: str):
+    def run(module, x, original):
+        if module.up_gate.bias is not None:
+            return original(x)
+        a = _rows(x)
+        b = module.up_gate.weight.to(torch.bfloat16).T
+        if not _served(_choice(a, b, plan_key, "swiglu")):
+            return original(x)
+        # Eager calls keep the eager BF16 rounding of the SiLU; traced calls follow the
+        # compiled arithmetic.
+        _packed, act = _planned_swiglu_mm(a, b, plan_key, not torch.compiler.is_compiling())
+        return module.down(act.reshape(*x.shape[:-1], module.down.in_features))
+    return run
 
 
 def apply_matmul_execution(model: torch.nn.Module, plan: MatmulPlan) -> None:
-    """Patch bias-free Linear and SwiGLU forwards inside ``model.cores``; apply before core
-    compilation and DDP (ops/matmul_execution.py:334-388). CPU/evaluation paths stay
-    original and parameters are never replaced by cached BF16 views."""
+    """Route the bias-free Linear and SwiGLU modules of ``model.cores`` through the plan
+    (ops/matmul_execution.py:334-388). Apply before compiling cores and before DDP.
+
+    Only training calls with gradients on CUDA tensors under BF16 autocast change path;
+    CPU and evaluation calls run the original forwards. Parameters stay the FP32 masters:
+    each forward casts them to BF16 inside the visible graph, so gradients reach the
+    masters through ordinary casts."""
     from warpstate.model import SwiGLU
 
     if not isinstance(plan, MatmulPlan):
         raise TypeError("Load a MatmulPlan before applying matrix execution")
     if getattr(model, "_matmul_execution_plan", None) is not None:
         raise ValueError("Matmul execution has already been applied")
-    if any(parameter.dtype != torch.float32 for parameter in model.parameters()):
+    if any(p.dtype != torch.float32 for p in model.parameters()):
         raise ValueError("Matmul execution requires FP32 master parameters")
     if plan.registry_key not in _PLANS:
         raise ValueError("Matmul plan is not registered in this process")
     model._matmul_execution_plan = plan
-    if not plan.entries:
-        return
-    has_fused = any(entry.kind == "swiglu" and entry.algorithm != "aten" for entry in plan.entries)
-
-    def bf16_training(module, x):
-        return (module.training and torch.is_grad_enabled() and x.is_cuda
-                and torch.is_autocast_enabled("cuda")
-                and torch.get_autocast_dtype("cuda") == torch.bfloat16)
-
+    swiglu = [e for e in plan.entries if e.kind == "swiglu"]
+    # SwiGLU modules are routed when the plan launches some fused kernel and has a SwiGLU
+    # entry of the module's widths; an ``aten`` entry then still selects the original.
+    fused_widths = ({(e.n, e.k) for e in swiglu}
+                    if any(e.algorithm != "aten" for e in swiglu) else set())
     for core in model.cores:
         for module in core.modules():
-            original = module.forward
             if (isinstance(module, torch.nn.Linear) and module.bias is None
                     and _linear_has_choices(module, plan)):
-                def linear_forward(x, _module=module, _original=original):
-                    if not bf16_training(_module, x):
-                        return _original(x)
-                    a = x.reshape(-1, x.shape[-1]).to(torch.bfloat16)
-                    b = _module.weight.to(torch.bfloat16).T
-                    output = _planned_mm(a, b, plan.registry_key)
-                    return output.reshape(*x.shape[:-1], _module.out_features)
-                module.forward = linear_forward
-            elif (isinstance(module, SwiGLU) and has_fused and any(
-                    entry.kind == "swiglu" and entry.n == module.up_gate.out_features
-                    and entry.k == module.up_gate.in_features for entry in plan.entries)):
-                def swiglu_forward(x, _module=module, _original=original):
-                    if not bf16_training(_module, x) or _module.up_gate.bias is not None:
-                        return _original(x)
-                    a = x.reshape(-1, x.shape[-1]).to(torch.bfloat16)
-                    b = _module.up_gate.weight.to(torch.bfloat16).T
-                    entry = _choice(a, b, plan.registry_key, "swiglu")
-                    if entry is None or entry.algorithm == "aten":
-                        return _original(x)
-                    _, activation = _planned_swiglu_mm(
-                        a, b, plan.registry_key, not torch.compiler.is_compiling())
-                    activation = activation.reshape(*x.shape[:-1], _module.down.in_features)
-                    return _module.down(activation)
-                module.forward = swiglu_forward
+                install_forward(module, _planned_linear(plan.registry_key))
+            elif (isinstance(module, SwiGLU) and (module.up_gate.out_features,
+                                                  module.up_gate.in_features) in fused_widths):
+                install_forward(module, _planned_swiglu(plan.registry_key))

@@ -64,6 +64,15 @@ class SwiGLU(nn.Module):
 
 
 class WarpStateCore(nn.Module):
+    """One core: norm1 -> in_proj -> (q, k, v, sigmoid(g), u) -> token mixer -> out_proj
+    with a residual add, then norm2 -> SwiGLU with a residual add
+    (warpstate/model.py:93-96, :107-112, :120-121, :174-178).
+
+    ``project`` and ``mix`` are the two halves of the token path: the fused-execution
+    adapter replaces ``project`` (RMSNorm prologue, projection and gate sigmoid in one
+    GEMM launch) and keeps ``mix``.
+    """
+
     def __init__(self, cfg: WarpStateConfig):
         super().__init__()
         d = cfg.d_model
@@ -73,11 +82,19 @@ class WarpStateCore(nn.Module):
         self.norm2 = RMSNorm(d, cfg.rms_eps)
         self.ffn = SwiGLU(d, cfg.ffn_hidden)
 
-    def forward(self, x: torch.Tensor) -> torch.Tensor:
+    def project(self, x: torch.Tensor) -> tuple[torch.Tensor, ...]:
+        """(q, k, v, sigmoid(g), u): the five d-wide slices of in_proj(norm1(x)), the fourth
+        through the gate sigmoid."""
         q, k, v, g, u = self.in_proj(self.norm1(x)).chunk(5, dim=-1)
-        gate = torch.sigmoid(g)
-        mixed = gate * v + (1 - gate) * torch.tanh(q * k + u)
-        x = x + self.out_proj(mixed)
+        return q, k, v, torch.sigmoid(g), u
+
+    def mix(self, q, k, v, gate, u) -> torch.Tensor:
+        """Placeholder token mixer (gate-weighted blend of v and a tanh of the other
+        slices) standing in for the reference's chunked attention and memory."""
+        return gate * v + (1 - gate) * torch.tanh(q * k + u)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        x = x + self.out_proj(self.mix(*self.project(x)))
         return x + self.ffn(self.norm2(x))
 
 
@@ -95,7 +112,9 @@ class WarpStateLM(nn.Module):
             if isinstance(module, (nn.Linear, nn.Embedding)):
                 nn.init.normal_(module.weight, mean=0.0, std=0.02)
 
-    def forward(self, input_ids, targets=None, *, return_logits=True):
+    def features(self, input_ids: torch.Tensor) -> torch.Tensor:
+        """Embedding, the depth loop over the shared cores and the final norm
+        (warpstate/model.py:303-313)."""
         x = self.embed(input_ids)
         for depth in range(self.cfg.logical_depth):
             x = x * (1.0 + self.depth_scale[depth]) + self.depth_bias[depth]
@@ -104,16 +123,24 @@ class WarpStateLM(nn.Module):
                 x = checkpoint(core, x, use_reentrant=False)
             else:
                 x = core(x)
-        x = self.final_norm(x)
+        return self.final_norm(x)
+
+    def chunked_loss(self, x: torch.Tensor, targets: torch.Tensor) -> torch.Tensor:
+        """Mean cross-entropy of the tied head over valid targets, one loss_chunk_size row
+        block of FP32 logits at a time (warpstate/model.py:314-334)."""
+        hidden = x.reshape(-1, x.size(-1))
+        labels = targets.reshape(-1)
+        loss = x.new_zeros((), dtype=torch.float32)
+        step = self.cfg.loss_chunk_size
+        for start in range(0, labels.numel(), step):
+            logits = F.linear(hidden[start:start + step], self.embed.weight).float()
+            loss = loss + F.cross_entropy(logits, labels[start:start + step], reduction="sum")
+        return loss / labels.ne(-100).sum().clamp_min(1)
+
+    def forward(self, input_ids, targets=None, *, return_logits=True):
+        x = self.features(input_ids)
         if targets is not None and not return_logits:
-            hidden = x.reshape(-1, x.size(-1))
-            labels = targets.reshape(-1)
-            loss = x.new_zeros((), dtype=torch.float32)
-            step = self.cfg.loss_chunk_size
-            for start in range(0, labels.numel(), step):
-                logits = F.linear(hidden[start:start + step], self.embed.weight).float()
-                loss = loss + F.cross_entropy(logits, labels[start:start + step], reduction="sum")
-            return None, loss / labels.ne(-100).sum().clamp_min(1)
+            return None, self.chunked_loss(x, targets)
         logits = F.linear(x, self.embed.weight)
         if targets is None:
             return logits
