@@ -196,7 +196,7 @@ int64_t ws_linear_ce_parts(int64_t vocab);
  * Fused LM-head cross-entropy forward. hidden [rows, d] (row stride ld_hidden, unit column
  * stride), weight [vocab, d] (nn.Embedding / tied head layout, row stride ld_weight),
  * int64 targets with -100 ignored. Writes per-token FP32 loss, lse, the target logit,
- * mean = sum(loss) / max(1, count) and count. `logits` (nullable): when given, the rounded
+ * mean = sum(loss) / max(1, count) and the int64 valid-token count. `logits` (nullable): when given, the rounded
  * BF16 logits are also stored there ([rows, vocab], row stride vocab; vocab % 4 == 0,
  * 16-byte aligned; both operands row-contiguous) for a backward that reads them instead
  * of recomputing the GEMM. Without it the logits exist only in registers.
@@ -206,7 +206,7 @@ int64_t ws_linear_ce_parts(int64_t vocab);
 int ws_linear_ce_forward(const void* hidden, int64_t ld_hidden, const void* weight,
                          int64_t ld_weight, const int64_t* targets, int64_t rows, int64_t vocab,
                          int64_t d, float* part_max, float* part_sum, float* target_logit,
-                         float* lse, float* loss, float* mean, float* count, void* logits,
+                         float* lse, float* loss, float* mean, int64_t* count, void* logits,
                          void* stream);
 
 /* Bytes of the workspace ws_linear_ce_backward needs for `chunk_rows`-row chunks. */
@@ -230,7 +230,7 @@ int64_t ws_linear_ce_workspace_bytes(int64_t rows, int64_t vocab, int64_t d, int
  */
 int ws_linear_ce_backward(const void* hidden, int64_t ld_hidden, const void* weight,
                           int64_t ld_weight, const void* weight_t, const int64_t* targets,
-                          const float* lse, const float* count, const float* grad_mean,
+                          const float* lse, const int64_t* count, const float* grad_mean,
                           int64_t rows, int64_t vocab, int64_t d, void* workspace,
                           int64_t chunk_rows, void* dhidden, int64_t ld_dhidden, float* dweight,
                           int64_t ld_dweight, const void* logits, void* stream);

@@ -287,3 +287,98 @@ def test_fused_entry_points_reject_cpu_tensors():
         fx.residual_mm(x, w, torch.zeros(4, 6, dtype=torch.bfloat16))
     with pytest.raises(ValueError, match="CUDA"):
         fx.linear_cross_entropy_forward(x, w, torch.zeros(4, dtype=torch.int64))
+
+
+def test_cross_entropy_state_must_match_the_operands():
+    """A state built for another row count or vocabulary is refused before any launch
+    (its buffers are indexed by the operands' rows and vocabulary)."""
+    from ops.fused_execution import CrossEntropyState, _check_state
+
+    state = CrossEntropyState(8, 64, "cpu")
+    _check_state(state, 8, 64, torch.device("cpu"))
+    for rows, vocab in ((16, 64), (8, 128), (4, 64)):
+        with pytest.raises(ValueError, match="CrossEntropyState"):
+            _check_state(state, rows, vocab, torch.device("cpu"))
+    state.lse = torch.empty(4)
+    with pytest.raises(ValueError, match="state.lse"):
+        _check_state(state, 8, 64, torch.device("cpu"))
+    with pytest.raises(TypeError):
+        _check_state(object(), 8, 64, torch.device("cpu"))
+
+
+def test_fused_output_buffers_are_checked_before_launch():
+    from ops.fused_execution import _check_buffer
+
+    good = torch.empty(4, 6, dtype=torch.bfloat16)
+    _check_buffer(good, (4, 6), torch.bfloat16, good.device, "out")
+    for bad in (torch.empty(4, 5, dtype=torch.bfloat16), torch.empty(4, 6),
+                torch.empty(6, 4, dtype=torch.bfloat16).T):
+        with pytest.raises(ValueError):
+            _check_buffer(bad, (4, 6), torch.bfloat16, good.device, "out")
+    # A row-strided view is fine where only a unit column stride is needed.
+    _check_buffer(torch.empty(4, 8, dtype=torch.bfloat16)[:, :6], (4, 6), torch.bfloat16,
+                  good.device, "out", contiguous=False)
+
+
+def _small_lm(**overrides):
+    torch.manual_seed(572)
+    cfg = dict(vocab_size=32, d_model=16, n_heads=2, n_cores=1, logical_depth=2,
+               ffn_hidden=24, chunk_size=4, gradient_checkpointing=False,
+               parallel_memory=True, loss_chunk_size=3)
+    cfg.update(overrides)
+    return WarpStateLM(WarpStateConfig(**cfg)).train()
+
+
+def test_fused_adapter_keeps_cpu_and_eval_paths_and_state():
+    """On the CPU (and in evaluation) the adapted model runs the original forwards: same
+    loss, same gradients, same parameters and state dict."""
+    from ops.fused_training import apply_fused_execution
+
+    reference = _small_lm()
+    adapted = copy.deepcopy(reference)
+    keys, params = tuple(adapted.state_dict()), tuple(adapted.parameters())
+    apply_fused_execution(adapted)
+    assert tuple(adapted.state_dict()) == keys
+    assert all(a is b for a, b in zip(params, adapted.parameters(), strict=True))
+    tokens = torch.randint(32, (2, 8))
+    labels = torch.randint(32, (2, 8))
+    labels.view(-1)[3:9] = -100
+    with torch.autocast("cpu", dtype=torch.bfloat16):
+        _, want = reference(tokens, labels, return_logits=False)
+        _, got = adapted(tokens, labels, return_logits=False)
+    assert torch.equal(got, want)
+    want.backward()
+    got.backward()
+    for p, q in zip(reference.parameters(), adapted.parameters(), strict=True):
+        assert torch.equal(p.grad, q.grad)
+    with pytest.raises(ValueError, match="already been applied"):
+        apply_fused_execution(adapted)
+    with pytest.raises(ValueError, match="FP32 master"):
+        apply_fused_execution(_small_lm().bfloat16())
+
+
+def test_bf16_residuals_make_the_stream_bf16_only_under_autocast():
+    from ops.residual_experiment import apply_bf16_residuals
+
+    reference = _small_lm()
+    model = copy.deepcopy(reference)
+    keys, params = tuple(model.state_dict()), tuple(model.parameters())
+    apply_bf16_residuals(model)
+    assert tuple(model.state_dict()) == keys
+    assert all(a is b for a, b in zip(params, model.parameters(), strict=True))
+    tokens = torch.randint(32, (2, 8))
+    # Outside autocast: the original forward, bit for bit.
+    assert torch.equal(model(tokens), reference(tokens))
+    seen = []
+    hook = model.cores[0].register_forward_pre_hook(lambda m, args: seen.append(args[0].dtype))
+    with torch.autocast("cpu", dtype=torch.bfloat16):
+        _, loss = model(tokens, tokens, return_logits=False)
+    hook.remove()
+    assert seen and all(dtype == torch.bfloat16 for dtype in seen)
+    loss.backward()
+    # Gradients reach the FP32 masters through the casts.
+    for name in ("embed.weight", "depth_scale", "depth_bias"):
+        grad = model.get_parameter(name).grad
+        assert grad is not None and grad.dtype == torch.float32
+    with pytest.raises(ValueError, match="already been applied"):
+        apply_bf16_residuals(model)

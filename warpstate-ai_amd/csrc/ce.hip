@@ -33,7 +33,7 @@ extern "C" int ws_linear_ce_forward(const void* hidden, int64_t ld_hidden, const
                                     int64_t ld_weight, const int64_t* targets, int64_t rows,
                                     int64_t vocab, int64_t d, float* part_max, float* part_sum,
                                     float* target_logit, float* lse, float* loss, float* mean,
-                                    float* count, void* logits, void* stream) {
+                                    int64_t* count, void* logits, void* stream) {
   if (int rc = check_ce(hidden, ld_hidden, weight, ld_weight, targets, rows, vocab, d)) return rc;
   if (!part_max || !part_sum || !target_logit || !lse || !loss || !mean || !count)
     return set_error(kInvalid, "null output pointer");
@@ -62,7 +62,7 @@ extern "C" int ws_linear_ce_forward(const void* hidden, int64_t ld_hidden, const
     if (int rc = dispatch_fast<false, FEpiCEStatsLogits>(p, am, bm, LaunchCfg{0, 1}, s)) return rc;
   } else if (fast_ok(p, am, bm, false)) {
     if (int rc = dispatch_fast<false, FEpiCEStats>(p, am, bm, LaunchCfg{0, 1}, s)) return rc;
-  } else if (int rc = dispatch<kMaskKK | kMaskGG, WS_TILE_ARGS_LARGE, false, false, EpiCEStats>(
+  } else if (int rc = dispatch<kMaskKK | kMaskGG, WS_TILE_ARGS_LARGE, false, EpiCEStats>(
                  p, am, bm, LaunchCfg{0, 1}, s)) {
     return rc;
   }
@@ -71,7 +71,8 @@ extern "C" int ws_linear_ce_forward(const void* hidden, int64_t ld_hidden, const
                      loss, (int)rows, (int)vocab);
   if (int rc = hip_check(hipGetLastError(), "ce combine launch")) return rc;
   hipLaunchKernelGGL(ce_mean_kernel, dim3(1), dim3(1024), 0, s, loss,
-                     reinterpret_cast<const long*>(targets), (int)rows, mean, count);
+                     reinterpret_cast<const long*>(targets), (int)rows, mean,
+                     reinterpret_cast<long*>(count));
   return hip_check(hipGetLastError(), "ce mean launch");
 }
 
@@ -99,7 +100,7 @@ extern "C" int64_t ws_linear_ce_workspace_bytes(int64_t rows, int64_t vocab, int
 extern "C" int ws_linear_ce_backward(const void* hidden, int64_t ld_hidden, const void* weight,
                                      int64_t ld_weight, const void* weight_t,
                                      const int64_t* targets, const float* lse,
-                                     const float* count, const float* grad_mean, int64_t rows,
+                                     const int64_t* count, const float* grad_mean, int64_t rows,
                                      int64_t vocab, int64_t d, void* workspace,
                                      int64_t chunk_rows, void* dhidden, int64_t ld_dhidden,
                                      float* dweight, int64_t ld_dweight, const void* logits,
@@ -125,7 +126,8 @@ extern "C" int ws_linear_ce_backward(const void* hidden, int64_t ld_hidden, cons
   float* scale_ws = reinterpret_cast<float*>(base);
   auto* gl = reinterpret_cast<unsigned short*>(base + 256);
   float* partials = reinterpret_cast<float*>(base + 256 + round256(chunk * vocab * 2));
-  hipLaunchKernelGGL(ce_scale_kernel, dim3(1), dim3(64), 0, s, grad_mean, count, scale_ws);
+  hipLaunchKernelGGL(ce_scale_kernel, dim3(1), dim3(64), 0, s, grad_mean,
+                     reinterpret_cast<const long*>(count), scale_ws);
   if (int rc = hip_check(hipGetLastError(), "ce scale launch")) return rc;
   for (long start = 0; start < rows; start += chunk) {
     const long r = rows - start < chunk ? rows - start : chunk;
@@ -150,7 +152,7 @@ extern "C" int ws_linear_ce_backward(const void* hidden, int64_t ld_hidden, cons
       if (int rc = hip_check(hipGetLastError(), "ce gradient launch")) return rc;
     } else if (fast_ok(p, am, bm, false)) {
       if (int rc = dispatch_fast<false, FEpiCEGrad>(p, am, bm, LaunchCfg{0, 1}, s)) return rc;
-    } else if (int rc = dispatch<kMaskKK | kMaskGG, WS_TILE_ARGS_LARGE, false, false, EpiCEGrad>(
+    } else if (int rc = dispatch<kMaskKK | kMaskGG, WS_TILE_ARGS_LARGE, false, EpiCEGrad>(
                    p, am, bm, LaunchCfg{0, 1}, s)) {
       return rc;
     }
@@ -167,7 +169,7 @@ extern "C" int ws_linear_ce_backward(const void* hidden, int64_t ld_hidden, cons
       const int wa = operand_mode(w.a, vocab, r, 256), wb = operand_mode(w.b, d, r, 256);
       if (fast_ok(w, wa, wb, false)) {
         if (int rc = dispatch_fast<false, FEpiAccF32<false>>(w, wa, wb, LaunchCfg{0, 1}, s)) return rc;
-      } else if (int rc = dispatch<kMaskMM, WS_TILE_ARGS_LARGE, false, false, EpiAccF32<false>>(
+      } else if (int rc = dispatch<kMaskMM, WS_TILE_ARGS_LARGE, false, EpiAccF32<false>>(
                      w, wa, wb, LaunchCfg{0, 1}, s)) {
         return rc;
       }
@@ -199,7 +201,7 @@ extern "C" int ws_linear_ce_backward(const void* hidden, int64_t ld_hidden, cons
       q.vec_out = (d % 4 == 0) && (ld_dhidden % 4 == 0) && (reinterpret_cast<unsigned long>(out) % 8 == 0);
       if (fast) {
         if (int rc = dispatch_fast<false, FEpiStore<false, false>>(q, qa, qb, LaunchCfg{0, 1}, s)) return rc;
-      } else if (int rc = dispatch<kMaskMM, WS_TILE_ARGS_LARGE, false, false, EpiStore<false, false>>(
+      } else if (int rc = dispatch<kMaskMM, WS_TILE_ARGS_LARGE, false, EpiStore<false, false>>(
                      q, qa, qb, LaunchCfg{0, 1}, s)) {
         return rc;
       }

@@ -21,6 +21,35 @@ static inline bool al(const void* p, int bytes) {
   return reinterpret_cast<unsigned long>(p) % bytes == 0;
 }
 
+namespace ws {
+// y = r(r(x rstd) r(w)) and rstd for rows of x (row stride ldx) into a contiguous y: the
+// RMSNorm pass before the fused input projection, also the eager standalone RMSNorm
+// forward. Rows of at most 4096 vector-aligned features stay in registers (x read once).
+int launch_rmsnorm_rows(const void* x, long ldx, const float* w, void* y, float* rstd, long m,
+                        long k, float eps, hipStream_t s) {
+  const int vec = (ldx % 8 == 0) && (k % 8 == 0) && al(x, 16) && al(y, 16);
+  const dim3 grid(cdiv(m, 4));
+  const auto* xs = static_cast<const unsigned short*>(x);
+  auto* ys = static_cast<unsigned short*>(y);
+  if (vec && k <= 512)
+    hipLaunchKernelGGL(rmsnorm_rows_reg_kernel<1>, grid, dim3(256), 0, s, xs, ldx, w, ys, rstd,
+                       (int)m, (int)k, eps);
+  else if (vec && k <= 1024)
+    hipLaunchKernelGGL(rmsnorm_rows_reg_kernel<2>, grid, dim3(256), 0, s, xs, ldx, w, ys, rstd,
+                       (int)m, (int)k, eps);
+  else if (vec && k <= 2048)
+    hipLaunchKernelGGL(rmsnorm_rows_reg_kernel<4>, grid, dim3(256), 0, s, xs, ldx, w, ys, rstd,
+                       (int)m, (int)k, eps);
+  else if (vec && k <= 4096)
+    hipLaunchKernelGGL(rmsnorm_rows_reg_kernel<8>, grid, dim3(256), 0, s, xs, ldx, w, ys, rstd,
+                       (int)m, (int)k, eps);
+  else
+    hipLaunchKernelGGL(rmsnorm_rows_kernel, grid, dim3(256), 0, s, xs, ldx, w, ys, rstd, (int)m,
+                       (int)k, eps, vec);
+  return hip_check(hipGetLastError(), "rmsnorm rows launch");
+}
+}  // namespace ws
+
 static int launch_rstd(const void* x, long ldx, float* rstd, long rows, long d, float eps,
                        hipStream_t s) {
   const int vec = (ldx % 8 == 0) && (d % 8 == 0) && al(x, 16);
@@ -50,26 +79,7 @@ extern "C" int ws_rmsnorm_gate_mm(const void* x, int64_t x_s0, const float* norm
   if (int rc = check_out_stride(n, 2, "output")) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
   // Prologue: one pass over x writes the normalized BF16 operand y and rstd.
-  const int vec = (x_s0 % 8 == 0) && (k % 8 == 0) && al(x, 16) && al(normed, 16);
-  const dim3 rgrid(cdiv(m, 4));
-  const auto* xs = static_cast<const unsigned short*>(x);
-  auto* ys = static_cast<unsigned short*>(normed);
-  if (vec && k <= 512)
-    hipLaunchKernelGGL(rmsnorm_rows_reg_kernel<1>, rgrid, dim3(256), 0, s, xs, (long)x_s0,
-                       norm_weight, ys, rstd, (int)m, (int)k, eps);
-  else if (vec && k <= 1024)
-    hipLaunchKernelGGL(rmsnorm_rows_reg_kernel<2>, rgrid, dim3(256), 0, s, xs, (long)x_s0,
-                       norm_weight, ys, rstd, (int)m, (int)k, eps);
-  else if (vec && k <= 2048)
-    hipLaunchKernelGGL(rmsnorm_rows_reg_kernel<4>, rgrid, dim3(256), 0, s, xs, (long)x_s0,
-                       norm_weight, ys, rstd, (int)m, (int)k, eps);
-  else if (vec && k <= 4096)
-    hipLaunchKernelGGL(rmsnorm_rows_reg_kernel<8>, rgrid, dim3(256), 0, s, xs, (long)x_s0,
-                       norm_weight, ys, rstd, (int)m, (int)k, eps);
-  else
-    hipLaunchKernelGGL(rmsnorm_rows_kernel, rgrid, dim3(256), 0, s, xs, (long)x_s0, norm_weight,
-                       ys, rstd, (int)m, (int)k, eps, vec);
-  if (int rc = hip_check(hipGetLastError(), "rmsnorm rows launch")) return rc;
+  if (int rc = launch_rmsnorm_rows(x, x_s0, norm_weight, normed, rstd, m, k, eps, s)) return rc;
   GemmParams p{};
   p.a = desc_a(normed, k, 1);
   p.b = desc_b(b, b_s0, b_s1);
@@ -82,7 +92,7 @@ extern "C" int ws_rmsnorm_gate_mm(const void* x, int64_t x_s0, const float* norm
   int am = operand_mode(p.a, m, k, 256), bm = operand_mode(p.b, n, k, 256);
   if (fast_ok(p, am, bm, false))
     return dispatch_fast<false, FEpiStore<true, false>>(p, am, bm, LaunchCfg{0, 1}, s);
-  return dispatch<kMaskMM, WS_TILE_ARGS_LARGE, false, false, EpiStore<true, false>>(p, am, bm,
+  return dispatch<kMaskMM, WS_TILE_ARGS_LARGE, false, EpiStore<true, false>>(p, am, bm,
                                                                                    LaunchCfg{0, 1}, s);
 }
 
@@ -108,7 +118,7 @@ extern "C" int ws_residual_mm(const void* a, int64_t a_s0, int64_t a_s1, const v
   if (fast_ok(p, am, bm, false))
     return dispatch_fast<false, FEpiStore<false, true>>(p, am, bm, LaunchCfg{0, 1}, s);
   constexpr unsigned mask = kMaskKK | ab_bit(kKContig, kMNContig) | kMaskGG;
-  return dispatch<mask, WS_TILE_ARGS_LARGE, false, false, EpiStore<false, true>>(
+  return dispatch<mask, WS_TILE_ARGS_LARGE, false, EpiStore<false, true>>(
       p, am, bm, LaunchCfg{0, 1}, s);
 }
 
@@ -135,7 +145,7 @@ extern "C" int ws_swiglu_backward_mm(const void* grad, int64_t g_s0, int64_t g_s
   if (fast_ok(p, am, bm, false))
     return dispatch_fast<false, FEpiSwigluBwd>(p, am, bm, LaunchCfg{0, 1}, s);
   constexpr unsigned mask = kMaskKK | ab_bit(kKContig, kMNContig) | kMaskGG;
-  return dispatch<mask, WS_TILE_ARGS_LARGE, false, false, EpiSwigluBwd>(
+  return dispatch<mask, WS_TILE_ARGS_LARGE, false, EpiSwigluBwd>(
       p, am, bm, LaunchCfg{0, 1}, s);
 }
 
@@ -251,7 +261,7 @@ extern "C" int ws_mm_accumulate_f32(const void* a, int64_t a_s0, int64_t a_s1, c
   if (splits <= 1) {
     if (fast_ok(p, am, bm, false))
       return dispatch_fast<false, FEpiAccF32<false>>(p, am, bm, LaunchCfg{0, 1}, s);
-    return dispatch<kMaskMM, WS_TILE_ARGS_LARGE, false, false, EpiAccF32<false>>(p, am, bm,
+    return dispatch<kMaskMM, WS_TILE_ARGS_LARGE, false, EpiAccF32<false>>(p, am, bm,
                                                                                   LaunchCfg{0, 1}, s);
   }
   const int workers = device_cus();
@@ -287,7 +297,7 @@ extern "C" int ws_mm_accumulate_f32(const void* a, int64_t a_s0, int64_t a_s1, c
   if (fast && p.vec_out) {
     if (int rc = dispatch_fast<false, FEpiAccF32<true>>(p, am, bm, LaunchCfg{0, (int)splits}, s))
       return rc;
-  } else if (int rc = dispatch<kMaskMM, WS_TILE_ARGS_LARGE, false, false, EpiAccF32<true>>(
+  } else if (int rc = dispatch<kMaskMM, WS_TILE_ARGS_LARGE, false, EpiAccF32<true>>(
                  p, am, bm, LaunchCfg{0, (int)splits}, s)) {
     return rc;
   }

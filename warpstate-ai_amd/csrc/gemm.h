@@ -5,7 +5,7 @@
 // Replaces the Triton kernels `_matmul_kernel` (ops/matmul_kernels.py:81-108),
 // `_persistent_tma_kernel` (ops/matmul_kernels.py:111-132) and
 // `_paired_swiglu_mm_kernel` (ops/matmul_epilogue.py:30-83), and adds the fused
-// pieces the reference composes from separate ops (RMSNorm prologue, gate sigmoid,
+// epilogues of the pieces the reference composes from separate ops (gate sigmoid,
 // residual add, SwiGLU backward, FP32 gradient accumulation, cross-entropy).
 //
 // Layout of one workgroup (BM x BN macro-tile, BK = 64):
@@ -71,7 +71,6 @@ struct GemmParams {
   unsigned short* c2; long ldc2;
   const unsigned short* aux; long ldaux;
   float* g; long ldg; long split_stride;
-  const float* rstd; const float* norm_w;
   int gate_lo, gate_hi;
   int eager;
   int round_acc;
@@ -302,40 +301,6 @@ struct TileLoader<R, NT, kGeneric, PAIRED> {
       u32x2_t w[8];
       transpose4x8(regs[i], w);
       store_units(lds, rc0 + i * (NT / 16), kq, w);
-    }
-  }
-};
-
-// --------------------------------------------------------------------------------------
-// RMSNorm prologue on a K-contiguous A tile: y = r(r(x * rstd[row]) * r(w[k]))
-// (warpstate/model.py:25-28 with BF16 input; the eager rounding of
-// ops/activation_execution.py:103-109).
-template <int R, int NT>
-struct RmsPrologue {
-  static constexpr int kPer = R * 8 / NT;
-  float rs[kPer];
-  float wb[8];
-  __device__ __forceinline__ void init_tile(const GemmParams& p, int row0, int tid) {
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-      int r = row0 + (tid >> 3) + i * (NT / 8);
-      rs[i] = r < p.M ? p.rstd[r] : 0.0f;
-    }
-  }
-  __device__ __forceinline__ void load_k(const GemmParams& p, int k0, int tid) {
-    int k = k0 + 8 * (tid & 7);
-#pragma unroll
-    for (int q = 0; q < 8; ++q) wb[q] = (k + q < p.K) ? rbf16(p.norm_w[k + q]) : 0.0f;
-  }
-  __device__ __forceinline__ void apply(u32x4_t (&regs)[kPer]) const {
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-#pragma unroll
-      for (int d = 0; d < 4; ++d) {
-        unsigned x = regs[i][d];
-        unsigned z = pack_bf16x2(lo_bf16(x) * rs[i], hi_bf16(x) * rs[i]);
-        regs[i][d] = pack_bf16x2(lo_bf16(z) * wb[2 * d], hi_bf16(z) * wb[2 * d + 1]);
-      }
     }
   }
 };
@@ -698,7 +663,7 @@ struct EpiCEGrad {
 // --------------------------------------------------------------------------------------
 // The kernel.
 
-template <int BM, int BN, int WM, int WN, int AMODE, int BMODE, bool PAIRED, bool RMS, class Epi>
+template <int BM, int BN, int WM, int WN, int AMODE, int BMODE, bool PAIRED, class Epi>
 __global__ void __launch_bounds__(WM * WN * kWave)
 gemm_kernel(const GemmParams p) {
   constexpr int NT = WM * WN * kWave;
@@ -706,7 +671,6 @@ gemm_kernel(const GemmParams p) {
   constexpr int FM = TM / 32, FN = TN / 32;
   static_assert(FM >= 1 && FN >= 1 && TM % 32 == 0 && TN % 32 == 0, "wave tile");
   static_assert(!PAIRED || (FN % 2 == 0), "paired tiles need up/gate block pairs");
-  static_assert(!RMS || AMODE == kKContig, "RMSNorm prologue reads K-contiguous A");
 
   extern __shared__ __attribute__((aligned(16))) unsigned short smem[];
   unsigned short* lds_a = smem;                    // [2][BM * BK]
@@ -719,7 +683,6 @@ gemm_kernel(const GemmParams p) {
 
   TileLoader<BM, NT, AMODE, false> la;
   TileLoader<BN, NT, BMODE, PAIRED> lb;
-  RmsPrologue<BM, NT> rms;
 
   // Per-lane LDS fragment row offsets (elements).
   int a_row[FM], b_row[FN];
@@ -752,7 +715,6 @@ gemm_kernel(const GemmParams p) {
 
     la.init(p.a, row0_a, p.M, 0, tid);
     lb.init(p.b, row0_b, PAIRED ? p.H : p.N, PAIRED ? p.H : 0, tid);
-    if (RMS) rms.init_tile(p, row0_a, tid);
 
     Acc<FM, FN> acc;
 #pragma unroll
@@ -765,10 +727,6 @@ gemm_kernel(const GemmParams p) {
     if (kt_begin < kt_end) {
       la.load(p.a, row0_a, kt_begin * kBK, p.K);
       lb.load(p.b, row0_b, kt_begin * kBK, p.K);
-      if constexpr (RMS) {
-        rms.load_k(p, kt_begin * kBK, tid);
-        rms.apply(la.regs);
-      }
       la.store(lds_a, tid);
       lb.store(lds_b, tid);
       __syncthreads();
@@ -779,7 +737,6 @@ gemm_kernel(const GemmParams p) {
         if (more) {
           la.load(p.a, row0_a, (kt + 1) * kBK, p.K);
           lb.load(p.b, row0_b, (kt + 1) * kBK, p.K);
-          if constexpr (RMS) rms.load_k(p, (kt + 1) * kBK, tid);
         }
         const unsigned short* sa = lds_a + cur * BM * kBK;
         const unsigned short* sb = lds_b + cur * BN * kBK;
@@ -798,7 +755,6 @@ gemm_kernel(const GemmParams p) {
               acc.v[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bf[j], af[i], acc.v[i][j], 0, 0, 0);
         }
         if (more) {
-          if constexpr (RMS) rms.apply(la.regs);
           la.store(lds_a + (cur ^ 1) * BM * kBK, tid);
           lb.store(lds_b + (cur ^ 1) * BN * kBK, tid);
         }

@@ -45,11 +45,11 @@ struct LaunchCfg {
   int workers;     // > 0: exactly this many workgroups (balanced accumulation)
 };
 
-template <int BM, int BN, int WM, int WN, int AM, int BMD, bool PAIRED, bool RMS, class Epi>
+template <int BM, int BN, int WM, int WN, int AM, int BMD, bool PAIRED, class Epi>
 int run_gemm(GemmParams p, LaunchCfg cfg, hipStream_t stream) {
   constexpr int NT = WM * WN * kWave;
   constexpr int lds = gemm_lds_bytes<BM, BN>();
-  const void* kern = reinterpret_cast<const void*>(&gemm_kernel<BM, BN, WM, WN, AM, BMD, PAIRED, RMS, Epi>);
+  const void* kern = reinterpret_cast<const void*>(&gemm_kernel<BM, BN, WM, WN, AM, BMD, PAIRED, Epi>);
   if (int rc = ensure_lds(kern, lds)) return rc;
   const int cols = PAIRED ? p.H : p.N;
   const int bn_cols = PAIRED ? BN / 2 : BN;
@@ -63,7 +63,7 @@ int run_gemm(GemmParams p, LaunchCfg cfg, hipStream_t stream) {
   const int resident = device_cus() * (lds > 80 * 1024 ? 1 : 2);
   dim3 grid(cfg.persistent ? (p.total_tiles < resident ? p.total_tiles : resident) : p.total_tiles,
             splits);
-  hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, AM, BMD, PAIRED, RMS, Epi>), grid, dim3(NT), lds,
+  hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, AM, BMD, PAIRED, Epi>), grid, dim3(NT), lds,
                      stream, p);
   return hip_check(hipGetLastError(), "gemm launch");
 }
@@ -88,7 +88,7 @@ constexpr unsigned kMaskMM = kMaskKK | ab_bit(kKContig, kMNContig) | ab_bit(kMNC
 
 // Runs the instantiation for (am, bm) if MASK holds it, demoting an operand to the
 // generic loader otherwise.
-template <unsigned MASK, int BM, int BN, int WM, int WN, bool PAIRED, bool RMS, class Epi>
+template <unsigned MASK, int BM, int BN, int WM, int WN, bool PAIRED, class Epi>
 int dispatch(const GemmParams& p, int am, int bm, LaunchCfg cfg, hipStream_t s) {
   auto has = [](int a, int b) { return (MASK & ab_bit(a, b)) != 0; };
   if (!has(am, bm)) {
@@ -99,7 +99,7 @@ int dispatch(const GemmParams& p, int am, int bm, LaunchCfg cfg, hipStream_t s) 
 #define WS_CASE(A_, B_)                                                            \
   case A_ * 3 + B_:                                                                \
     if constexpr ((MASK & ab_bit(A_, B_)) != 0)                                    \
-      return run_gemm<BM, BN, WM, WN, A_, B_, PAIRED, RMS, Epi>(p, cfg, s);        \
+      return run_gemm<BM, BN, WM, WN, A_, B_, PAIRED, Epi>(p, cfg, s);             \
     break;
   switch (am * 3 + bm) {
     WS_CASE(0, 0) WS_CASE(0, 1) WS_CASE(0, 2)

@@ -54,8 +54,8 @@ extern "C" int ws_mm(const void* a, int64_t a_s0, int64_t a_s1, const void* b, i
   if (tile == kTileLarge && fast_ok(p, am, bm, false))
     return dispatch_fast<false, FEpiStore<false, false>>(p, am, bm, cfg, s);
   if (tile == kTileLarge)
-    return dispatch<kMaskMM, WS_TILE_ARGS_LARGE, false, false, EpiStore<false, false>>(p, am, bm, cfg, s);
-  return dispatch<kMaskMM, WS_TILE_ARGS_SMALL, false, false, EpiStore<false, false>>(p, am, bm, cfg, s);
+    return dispatch<kMaskMM, WS_TILE_ARGS_LARGE, false, EpiStore<false, false>>(p, am, bm, cfg, s);
+  return dispatch<kMaskMM, WS_TILE_ARGS_SMALL, false, EpiStore<false, false>>(p, am, bm, cfg, s);
 }
 
 extern "C" int ws_swiglu_mm(const void* a, int64_t a_s0, int64_t a_s1, const void* b,
@@ -90,6 +90,6 @@ extern "C" int ws_swiglu_mm(const void* a, int64_t a_s0, int64_t a_s1, const voi
   if (tile == kTileLarge && fast_ok(p, am, bm, true))
     return dispatch_fast<true, FEpiSwiglu>(p, am, bm, cfg, s);
   if (tile == kTileLarge)
-    return dispatch<kMaskKK | kMaskGG, WS_TILE_ARGS_LARGE, true, false, EpiSwiglu>(p, am, bm, cfg, s);
-  return dispatch<kMaskKK | kMaskGG, WS_TILE_ARGS_SMALL, true, false, EpiSwiglu>(p, am, bm, cfg, s);
+    return dispatch<kMaskKK | kMaskGG, WS_TILE_ARGS_LARGE, true, EpiSwiglu>(p, am, bm, cfg, s);
+  return dispatch<kMaskKK | kMaskGG, WS_TILE_ARGS_SMALL, true, EpiSwiglu>(p, am, bm, cfg, s);
 }

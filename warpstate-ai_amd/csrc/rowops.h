@@ -378,18 +378,20 @@ static __global__ void __launch_bounds__(256) ce_combine_kernel(const float* __r
 }
 
 // Mean over valid tokens, sum(loss) / max(1, count(target != -100)) (warpstate/model.py:334,
-// ops/loss_experiment.py:18-19). One block; a fixed reduction order makes it deterministic.
-// Also writes the backward scale dmean / max(1, count) when dmean is given.
+// ops/loss_experiment.py:18-19). One block; a fixed reduction order makes the FP32 sum
+// deterministic. The valid-token count is an integer, exact for any row count; like the
+// reference's FP32 / int64 division it is converted to FP32 for the quotient.
 static __global__ void __launch_bounds__(1024) ce_mean_kernel(const float* __restrict__ loss,
                                                        const long* __restrict__ targets, int rows,
                                                        float* __restrict__ mean,
-                                                       float* __restrict__ count_out) {
+                                                       long* __restrict__ count_out) {
   __shared__ float ssum[1024];
-  __shared__ float scnt[1024];
-  float s = 0.0f, c = 0.0f;
+  __shared__ long scnt[1024];
+  float s = 0.0f;
+  long c = 0;
   for (int i = threadIdx.x; i < rows; i += 1024) {
     s += loss[i];
-    c += targets[i] != -100 ? 1.0f : 0.0f;
+    c += targets[i] != -100 ? 1 : 0;
   }
   ssum[threadIdx.x] = s;
   scnt[threadIdx.x] = c;
@@ -402,16 +404,16 @@ static __global__ void __launch_bounds__(1024) ce_mean_kernel(const float* __res
     __syncthreads();
   }
   if (threadIdx.x == 0) {
-    float cnt = scnt[0];
-    mean[0] = ssum[0] / fmaxf(cnt, 1.0f);
+    const long cnt = scnt[0];
+    mean[0] = ssum[0] / (float)(cnt > 1 ? cnt : 1);
     count_out[0] = cnt;
   }
 }
 
 // Backward scale of the summed cross-entropy: dmean / max(1, count).
-static __global__ void ce_scale_kernel(const float* __restrict__ dmean, const float* __restrict__ count,
+static __global__ void ce_scale_kernel(const float* __restrict__ dmean, const long* __restrict__ count,
                                 float* __restrict__ scale) {
-  if (threadIdx.x == 0) scale[0] = dmean[0] / fmaxf(count[0], 1.0f);
+  if (threadIdx.x == 0) scale[0] = dmean[0] / (float)(count[0] > 1 ? count[0] : 1);
 }
 
 // ---------------------------------------------------------------------------------------

@@ -3,6 +3,11 @@
 #include "launch.h"
 #include "rowops.h"
 
+namespace ws {
+int launch_rmsnorm_rows(const void* x, long ldx, const float* w, void* y, float* rstd, long m,
+                        long k, float eps, hipStream_t s);
+}
+
 using namespace ws;
 
 extern "C" int ws_swiglu_forward(const void* packed, void* out, int64_t rows, int64_t h,
@@ -36,6 +41,10 @@ extern "C" int ws_rmsnorm_forward(const void* x, const float* weight, void* y, f
   if (!x || !weight || !y || !rstd) return set_error(kInvalid, "null pointer");
   if (rows < 0 || d < 1 || !fits_i32(rows) || !fits_i32(d)) return set_error(kInvalid, "invalid RMSNorm shape");
   if (rows == 0) return kOk;
+  // Eager rounding is the arithmetic of the fused projection's row pass: same kernel.
+  if (eager_rounding)
+    return launch_rmsnorm_rows(x, d, weight, y, rstd, rows, d, eps,
+                               static_cast<hipStream_t>(stream));
   hipLaunchKernelGGL(rmsnorm_fwd_kernel, dim3(cdiv(rows, 4)), dim3(256), 0,
                      static_cast<hipStream_t>(stream), static_cast<const unsigned short*>(x), weight,
                      static_cast<unsigned short*>(y), rstd, (int)rows, (int)d, eps,

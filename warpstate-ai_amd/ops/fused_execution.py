@@ -3,10 +3,12 @@
 The reference composes these from separate operators; here each is one GEMM launch whose
 prologue or epilogue does the extra work in registers:
 
-* ``rmsnorm_gate_mm``: RMSNorm (warpstate/model.py:22-28) as the prologue of the fused
-  input projection (warpstate/model.py:93,109), with sigmoid on the gate column range
-  (warpstate/model.py:174). A row-statistics pass (one read of x) precedes the GEMM; the
-  normalized operand is formed while the A tile is staged and never stored.
+* ``rmsnorm_gate_mm``: RMSNorm (warpstate/model.py:22-28) before the fused input
+  projection (warpstate/model.py:93,109), with sigmoid on the gate column range
+  (warpstate/model.py:174) in the GEMM's epilogue. A row pass (x read once, held in
+  registers) writes the normalized rows y and rstd; the GEMM then reads y. y has to reach
+  HBM anyway, as the saved input of the projection's weight gradient, and its per-element
+  BF16 roundings r(r(x rstd) r(w)) keep rstd from being factored out of the product.
 * ``residual_mm``: down projection plus the BF16 residual add (warpstate/model.py:178,
   ops/residual_experiment.py:25-58).
 * ``swiglu_backward_mm``: the down projection's input gradient (ops/matmul_execution.py:239)
@@ -37,6 +39,20 @@ def _check_bf16_cuda(*tensors):
             raise ValueError("Fused matrix kernels require CUDA tensors")
         if tensor.dtype != torch.bfloat16:
             raise ValueError("Fused matrix kernels require BF16 operands")
+
+
+def _check_buffer(t: torch.Tensor, shape: tuple, dtype: torch.dtype, device: torch.device,
+                  name: str, contiguous: bool = True) -> None:
+    """A caller-supplied output or workspace must have exactly the shape, dtype and device
+    the launch writes, and be contiguous (or, with ``contiguous=False``, have a unit
+    column stride), so that no kernel writes outside it."""
+    if tuple(t.shape) != tuple(shape) or t.dtype != dtype or t.device != device:
+        raise ValueError(f"{name} must be a {str(dtype).removeprefix('torch.')} tensor of "
+                         f"shape {list(shape)} on {device}")
+    if contiguous and not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    if not contiguous and t.ndim == 2 and t.stride(1) != 1:
+        raise ValueError(f"{name} must have a unit column stride")
 
 
 # Rows of A from which a transposed copy of an N-contiguous B pays for itself: the copy
@@ -102,14 +118,19 @@ def rmsnorm_gate_mm(x: torch.Tensor, norm_weight: torch.Tensor, eps: float,
         raise ValueError("RMSNorm weight must be a contiguous FP32 vector")
     m, k = x.shape
     n = weight.shape[0]
+    if norm_weight.shape != (k,) or norm_weight.device != x.device:
+        raise ValueError("RMSNorm weight must have one FP32 value per feature, on x's device")
+    if not 0 <= gate[0] <= gate[1] <= n:
+        raise ValueError(f"gate columns {tuple(gate)} outside [0, {n}]")
     if out is None:
         out = torch.empty((m, n), dtype=torch.bfloat16, device=x.device)
+    _check_buffer(out, (m, n), torch.bfloat16, x.device, "out")
     if rstd is None:
         rstd = torch.empty((m,), dtype=torch.float32, device=x.device)
+    _check_buffer(rstd, (m,), torch.float32, x.device, "rstd")
     if normed is None:
         normed = torch.empty((m, k), dtype=torch.bfloat16, device=x.device)
-    elif normed.shape != (m, k) or not normed.is_contiguous() or normed.dtype != torch.bfloat16:
-        raise ValueError("normed must be a contiguous BF16 [M, K] tensor")
+    _check_buffer(normed, (m, k), torch.bfloat16, x.device, "normed")
     b = weight.T
     _hip.call("ws_rmsnorm_gate_mm", x.data_ptr(), x.stride(0), norm_weight.data_ptr(),
               float(eps), rstd.data_ptr(), normed.data_ptr(), b.data_ptr(), b.stride(0),
@@ -126,7 +147,10 @@ def sigmoid_backward_cols(dout: torch.Tensor, out: torch.Tensor, gate: tuple[int
         raise ValueError("dout and out must be matching [M, N] tensors with unit column stride")
     if dp is None:
         dp = torch.empty_like(dout)
+    _check_buffer(dp, dout.shape, torch.bfloat16, dout.device, "dp", contiguous=False)
     rows, cols = dout.shape
+    if not 0 <= gate[0] <= gate[1] <= cols:
+        raise ValueError(f"gate columns {tuple(gate)} outside [0, {cols}]")
     _hip.call("ws_sigmoid_backward_cols", dout.data_ptr(), dout.stride(0), out.data_ptr(),
               out.stride(0), dp.data_ptr(), dp.stride(0), rows, cols, int(gate[0]),
               int(gate[1]), _hip.stream(dout))
@@ -165,6 +189,7 @@ def residual_mm(a: torch.Tensor, weight: torch.Tensor, residual: torch.Tensor,
         raise ValueError("Expected a [M, K], weight [N, K] and a row-major residual [M, N]")
     if out is None:
         out = torch.empty((m, n), dtype=torch.bfloat16, device=a.device)
+    _check_buffer(out, (m, n), torch.bfloat16, a.device, "out")
     b = weight.T
     _hip.call("ws_residual_mm", a.data_ptr(), a.stride(0), a.stride(1), b.data_ptr(),
               b.stride(0), b.stride(1), residual.data_ptr(), residual.stride(0),
@@ -184,6 +209,7 @@ def swiglu_backward_mm(grad: torch.Tensor, down_weight: torch.Tensor, packed: to
         raise ValueError("Expected dY [M, d], down weight [d, H], contiguous packed [M, 2H]")
     if out is None:
         out = torch.empty((m, 2 * h), dtype=torch.bfloat16, device=grad.device)
+    _check_buffer(out, (m, 2 * h), torch.bfloat16, grad.device, "out")
     down_weight = k_contiguous_b(down_weight, m)
     _hip.call("ws_swiglu_backward_mm", grad.data_ptr(), grad.stride(0), grad.stride(1),
               down_weight.data_ptr(), down_weight.stride(0), down_weight.stride(1),
@@ -284,7 +310,7 @@ class CrossEntropyState:
         self.lse = torch.empty((rows,), **f32)
         self.loss = torch.empty((rows,), **f32)
         self.mean = torch.empty((), **f32)
-        self.count = torch.empty((), **f32)
+        self.count = torch.empty((), dtype=torch.int64, device=device)
         self.rows, self.vocab = rows, vocab
         self.chunk_rows = min(chunk_rows, rows)
         self.logits = (torch.empty((rows, vocab), dtype=torch.bfloat16, device=device)
@@ -313,6 +339,31 @@ def _check_ce(hidden, weight, targets):
         raise ValueError("Targets must be a contiguous int64 vector, one per row")
 
 
+def _check_state(state: CrossEntropyState, rows: int, vocab: int, device) -> None:
+    """The state's buffers are indexed by the operands' rows and vocabulary: a state built
+    for another shape or device would be written out of bounds, so it is refused."""
+    if not isinstance(state, CrossEntropyState):
+        raise TypeError("state must be a CrossEntropyState")
+    if (state.rows, state.vocab) != (rows, vocab):
+        raise ValueError(f"CrossEntropyState was built for {state.rows} rows and vocabulary "
+                         f"{state.vocab}, not {rows} and {vocab}")
+    if state.lse.device != device:
+        raise ValueError("CrossEntropyState buffers are on another device")
+    parts = _hip.query("ws_linear_ce_parts", vocab)
+    for name, buffer, shape, dtype in (("part_max", state.part_max, (rows, parts), torch.float32),
+                                       ("part_sum", state.part_sum, (rows, parts), torch.float32),
+                                       ("target_logit", state.target_logit, (rows,), torch.float32),
+                                       ("lse", state.lse, (rows,), torch.float32),
+                                       ("loss", state.loss, (rows,), torch.float32),
+                                       ("mean", state.mean, (), torch.float32),
+                                       ("count", state.count, (), torch.int64)):
+        _check_buffer(buffer, shape, dtype, device, "state." + name)
+    if state.logits is not None:
+        _check_buffer(state.logits, (rows, vocab), torch.bfloat16, device, "state.logits")
+    if not 1 <= state.chunk_rows <= rows:
+        raise ValueError("CrossEntropyState chunk_rows must lie in [1, rows]")
+
+
 def linear_cross_entropy_forward(hidden: torch.Tensor, weight: torch.Tensor,
                                  targets: torch.Tensor, state: CrossEntropyState | None = None
                                  ) -> CrossEntropyState:
@@ -323,6 +374,7 @@ def linear_cross_entropy_forward(hidden: torch.Tensor, weight: torch.Tensor,
     vocab = weight.shape[0]
     if state is None:
         state = CrossEntropyState(rows, vocab, hidden.device)
+    _check_state(state, rows, vocab, hidden.device)
     _hip.call("ws_linear_ce_forward", hidden.data_ptr(), hidden.stride(0), weight.data_ptr(),
               weight.stride(0), targets.data_ptr(), rows, vocab, d, state.part_max.data_ptr(),
               state.part_sum.data_ptr(), state.target_logit.data_ptr(), state.lse.data_ptr(),
@@ -344,16 +396,19 @@ def linear_cross_entropy_backward(hidden: torch.Tensor, weight: torch.Tensor,
     _check_ce(hidden, weight, targets)
     rows, d = hidden.shape
     vocab = weight.shape[0]
+    _check_state(state, rows, vocab, hidden.device)
+    if grad_mean.numel() != 1 or grad_mean.device != hidden.device:
+        raise ValueError("grad_mean must be one value on the operands' device")
     grad_mean = grad_mean.reshape(1).to(torch.float32).contiguous()
     if out is None:
         out = torch.empty((rows, d), dtype=torch.bfloat16, device=hidden.device)
+    _check_buffer(out, (rows, d), torch.bfloat16, hidden.device, "out", contiguous=False)
+    if weight_grad is not None:
+        _check_buffer(weight_grad, (vocab, d), torch.float32, hidden.device, "weight_grad",
+                      contiguous=False)
     workspace = state.backward_workspace(d)
     # The dHidden GEMM reads the head weight along the vocabulary: give it W^T rows.
     weight_t = transpose(weight) if rows >= TRANSPOSE_MIN_ROWS else None
-    if weight_grad is not None and (weight_grad.dtype != torch.float32
-                                    or weight_grad.shape != (vocab, d)
-                                    or weight_grad.stride(1) != 1):
-        raise ValueError("weight_grad must be an FP32 [vocab, d] tensor with unit column stride")
     _hip.call("ws_linear_ce_backward", hidden.data_ptr(), hidden.stride(0), weight.data_ptr(),
               weight.stride(0), None if weight_t is None else weight_t.data_ptr(),
               targets.data_ptr(), state.lse.data_ptr(), state.count.data_ptr(),
@@ -365,29 +420,51 @@ def linear_cross_entropy_backward(hidden: torch.Tensor, weight: torch.Tensor,
     return out
 
 
-class LinearCrossEntropy(torch.autograd.Function):
-    """mean cross-entropy of r(hidden @ weight.T) with the gradient to ``hidden``.
+def _bf16_rows(t: torch.Tensor) -> torch.Tensor:
+    """BF16 copy (or the tensor itself) with a unit column stride, as the kernels take."""
+    t = t.to(torch.bfloat16)
+    return t if t.stride(-1) == 1 else t.contiguous()
 
-    The tied weight receives no gradient from this function."""
+
+class LinearCrossEntropy(torch.autograd.Function):
+    """(mean, per-token loss) of cross-entropy over r(hidden @ weight.T), the tied LM head
+    of warpstate/model.py:316-334, with gradients to ``hidden`` and ``weight``.
+
+    ``hidden`` [rows, d] and ``weight`` [vocab, d] may be BF16 or FP32; FP32 operands are
+    rounded to BF16 first, as F.linear under BF16 autocast does. The weight's gradient is
+    accumulated in FP32 chunk by chunk, sum_c f32(r(G_c^T h_c)); an FP32 weight (the
+    master parameter) receives that FP32 sum, a BF16 weight its BF16 rounding. The
+    per-token loss is not differentiable."""
 
     @staticmethod
-    def forward(ctx, hidden, weight, targets):
-        state = linear_cross_entropy_forward(hidden, weight, targets)
-        ctx.save_for_backward(hidden, weight, targets)
+    def forward(ctx, hidden, weight, targets, chunk_rows=DEFAULT_CE_CHUNK_ROWS):
+        h, w = _bf16_rows(hidden), _bf16_rows(weight)
+        state = CrossEntropyState(h.shape[0], w.shape[0], h.device, chunk_rows)
+        linear_cross_entropy_forward(h, w, targets, state)
+        ctx.save_for_backward(h, w, targets)
         ctx.state = state
+        ctx.dtypes = (hidden.dtype, weight.dtype)
         ctx.mark_non_differentiable(state.loss)
         return state.mean.clone(), state.loss
 
     @staticmethod
     def backward(ctx, grad_mean, _grad_loss):
-        hidden, weight, targets = ctx.saved_tensors
-        dhidden = linear_cross_entropy_backward(hidden, weight, targets, ctx.state, grad_mean)
-        return dhidden, None, None
+        h, w, targets = ctx.saved_tensors
+        if grad_mean is None:
+            grad_mean = torch.zeros((), dtype=torch.float32, device=h.device)
+        want_h, want_w = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        weight_grad = (torch.zeros(w.shape, dtype=torch.float32, device=w.device)
+                       if want_w else None)
+        dh = linear_cross_entropy_backward(h, w, targets, ctx.state, grad_mean,
+                                           weight_grad=weight_grad)
+        hidden_dtype, weight_dtype = ctx.dtypes
+        return (dh.to(hidden_dtype) if want_h else None,
+                weight_grad.to(weight_dtype) if want_w else None, None, None)
 
 
-def linear_cross_entropy(hidden, weight, targets):
-    """(mean, per-token loss) with autograd to ``hidden``."""
-    return LinearCrossEntropy.apply(hidden, weight, targets)
+def linear_cross_entropy(hidden, weight, targets, chunk_rows=DEFAULT_CE_CHUNK_ROWS):
+    """(mean, per-token loss) of the fused LM head, with autograd to hidden and weight."""
+    return LinearCrossEntropy.apply(hidden, weight, targets, chunk_rows)
 
 
 def mlp_backward(x: torch.Tensor, w_upgate: torch.Tensor, w_down: torch.Tensor,
