@@ -88,6 +88,21 @@ int ws_rmsnorm_backward(const void* x, const float* weight, const float* rstd, c
                         void* dx, float* dweight, float* partial, int64_t rows, int64_t d,
                         int eager_rounding, void* stream);
 
+/* Allocation-free variant of ws_rmsnorm_backward: the same kernels and results, with the
+ * weight-gradient partials in a static 4 MiB device array of the library instead of a
+ * caller workspace. No counterpart in the reference: it is for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). It calls no allocator. Limit: ceil(rows / 32) * d <=
+ * ws_rmsnorm_backward_static_max_partial_floats() (2^20; e.g. 16384 x 2048), larger
+ * sizes return an error. Each GPU holds its own copy of the array until the process
+ * ends; calls that overlap on one GPU share it and race. */
+int ws_rmsnorm_backward_static(const void* x, const float* weight, const float* rstd,
+                               const void* grad, void* dx, float* dweight, int64_t rows,
+                               int64_t d, int eager_rounding, void* stream);
+
+/* Partial floats the static scratch of ws_rmsnorm_backward_static holds. */
+int64_t ws_rmsnorm_backward_static_max_partial_floats(void);
+
 /* out[cols, rows] = transpose(in[rows, cols]) for BF16 (in has row stride ld_in, out is
  * contiguous). Used to give weight-side GEMM operands a contiguous reduction dimension:
  * the input gradient dX = dY @ W (ops/matmul_execution.py:239) then reads W^T rows.

@@ -1,4 +1,6 @@
 // C ABI: standalone SwiGLU and RMSNorm kernels (ops/activation_execution.py).
+#include <mutex>
+
 #include "../../include/warpstate_hip.h"
 #include "launch.h"
 #include "rowops.h"
@@ -69,9 +71,9 @@ static int launch_rms_bwd(const void* x, const float* weight, const float* rstd,
   return hip_check(hipGetLastError(), "rmsnorm backward launch");
 }
 
-extern "C" int ws_rmsnorm_backward(const void* x, const float* weight, const float* rstd,
-                                   const void* grad, void* dx, float* dweight, float* partial,
-                                   int64_t rows, int64_t d, int eager_rounding, void* stream) {
+static int rmsnorm_backward(const void* x, const float* weight, const float* rstd,
+                            const void* grad, void* dx, float* dweight, float* partial,
+                            int64_t rows, int64_t d, int eager_rounding, void* stream) {
   if (!x || !weight || !rstd || !grad || !dx || !dweight || !partial)
     return set_error(kInvalid, "null pointer");
   if (rows < 1 || d < 1 || !fits_i32(rows) || !fits_i32(d)) return set_error(kInvalid, "invalid RMSNorm shape");
@@ -94,6 +96,70 @@ extern "C" int ws_rmsnorm_backward(const void* x, const float* weight, const flo
   hipLaunchKernelGGL(rms_weight_reduce_kernel, dim3(cdiv(d, kRmsReduceCols)), dim3(256), 0, s, partial,
                      dweight, groups, (int)d, e);
   return hip_check(hipGetLastError(), "rmsnorm weight reduce launch");
+}
+
+extern "C" int ws_rmsnorm_backward(const void* x, const float* weight, const float* rstd,
+                                   const void* grad, void* dx, float* dweight, float* partial,
+                                   int64_t rows, int64_t d, int eager_rounding, void* stream) {
+  return rmsnorm_backward(x, weight, rstd, grad, dx, dweight, partial, rows, d, eager_rounding,
+                          stream);
+}
+
+// ---------------------------------------------------------------------------------------
+// Allocation-free RMSNorm backward. Its weight-gradient partials live in `scratch`, a
+// file-scope device array that every GPU the library runs on holds until the process ends.
+// In host code `scratch` names a host-side stand-in, not device memory: its device address
+// comes from hipGetSymbolAddress, once per device (with that device current), and only
+// that address is passed to kernels. The kernels write every partial they later read, so
+// the array needs no clearing; calls that overlap on one GPU share it and race.
+namespace {
+
+constexpr long kStaticPartialFloats = 1L << 20;  // 4 MiB: rows x d up to 2^25 at d % 8 == 0
+__device__ __align__(256) float scratch[kStaticPartialFloats];
+
+constexpr int kScratchDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[kScratchDevices];
+
+int scratch_partials(float** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return set_error(kHipError, "hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kScratchDevices) return set_error(kInvalid, "device %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return set_error(kHipError, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+    g_scratch_ptr[dev] = static_cast<float*>(p);
+  }
+  *out = g_scratch_ptr[dev];
+  return kOk;
+}
+
+}  // namespace
+
+extern "C" int64_t ws_rmsnorm_backward_static_max_partial_floats(void) {
+  return kStaticPartialFloats;
+}
+
+extern "C" int ws_rmsnorm_backward_static(const void* x, const float* weight, const float* rstd,
+                                          const void* grad, void* dx, float* dweight,
+                                          int64_t rows, int64_t d, int eager_rounding,
+                                          void* stream) {
+  if (rows < 1 || d < 1 || !fits_i32(rows) || !fits_i32(d))
+    return set_error(kInvalid, "invalid RMSNorm shape");
+  const long need = ws_rmsnorm_backward_partial_floats(rows, d);
+  if (need > kStaticPartialFloats)
+    return set_error(kInvalid,
+                     "RMSNorm backward of %ld x %ld needs %ld partial floats; the static scratch "
+                     "holds %ld (use ws_rmsnorm_backward with a workspace)",
+                     (long)rows, (long)d, need, kStaticPartialFloats);
+  float* partial = nullptr;
+  if (int rc = scratch_partials(&partial)) return rc;
+  return rmsnorm_backward(x, weight, rstd, grad, dx, dweight, partial, rows, d, eager_rounding,
+                          stream);
 }
 
 extern "C" int ws_transpose_bf16(const void* in, int64_t ld_in, void* out, int64_t rows,
