@@ -16,9 +16,12 @@ HBM:
 
 ``value`` is the step's algorithmic FLOPs over its wall time (TFLOP/s). The other two
 configurations are timed beside it and reported under ``per_config``: config 1 (SwiGLU
-4096 x 1024 -> 2 x 2816) and config 5 (LM head with fused cross-entropy, forward
-statistics + dHidden, 16384 x 2048 -> 32768, once with the logits only in registers and
-once with the forward storing them for the backward).
+4096 x 1024 -> 2 x 2816) and config 5 (LM head with fused cross-entropy, 16384 x 2048 ->
+32768: the one-pass fused loss, whose logits exist one 8192-row chunk at a time, and the
+two-pass variant that keeps the logits only in registers and recomputes them). The
+HBM-bound passes (the RMSNorm row pass, the RMSNorm backward, the LM-head combine and
+logit-gradient passes, the attention-backward layout) are timed alone under
+``hbm_parts``.
 
 ``roofline`` describes the dominant kernel of the step (the FP32-accumulating wgrad GEMM
 of the MLP backward by default); its average launch time comes from HIP events around
@@ -121,8 +124,13 @@ def gpu_inputs(m, device):
     return dev
 
 
-def run_step(inp, out, timer=None):
-    """One hot-path pass; every kernel launches through the C ABI on the current stream."""
+def run_step(inp, out, dp, timer=None):
+    """One hot-path pass; every kernel launches through the C ABI on the current stream.
+
+    ``dp`` is this step's incoming gradient of the input projection's output. The QKV
+    backward applies the gate-sigmoid backward to it in place (rmsnorm_gate_mm_backward
+    with in_place=True: autograd hands the gradient over and frees it after this use), so
+    every step gets its own fresh copy (``fresh_gradients``)."""
     from contextlib import nullcontext
 
     from ops.activation_execution import _rms_backward
@@ -153,12 +161,18 @@ def run_step(inp, out, timer=None):
         # Backward of RMSNorm -> projection -> gate sigmoid (rmsnorm_gate_mm_backward with
         # in_place=True): the incoming gradient of the projection output has no other
         # consumer, so the sigmoid backward rewrites its gate columns in place.
-        dp = sigmoid_backward_cols(inp["qkv_dp"], out["qkv"], GATE, inp["qkv_dp"])
+        dp = sigmoid_backward_cols(dp, out["qkv"], GATE, dp)
         with reg("qkv_bwd.dx"):
             dy = mm(dp, inp["qkv_w"])
         with reg("qkv_bwd.wgrad"):
             mm_accumulate_(inp["qkv_g"], dp.T, out["qkv_z"], True)
         _rms_backward(inp["qkv_x"], inp["qkv_norm_weight"], out["rstd"], dy, True)
+
+
+def fresh_gradients(inp, count):
+    """``count`` copies of the pristine incoming gradient, made before a timed loop so
+    that each step's in-place sigmoid backward starts from the same values."""
+    return [inp["qkv_dp"].clone() for _ in range(count)]
 
 
 def bench_gpu(args):
@@ -171,20 +185,23 @@ def bench_gpu(args):
            "dpacked": torch.empty((m, 2 * FFN), dtype=torch.bfloat16, device=device),
            # The normalized input the forward saves for the wgrad of the input projection.
            "qkv_z": torch.empty((m, D), dtype=torch.bfloat16, device=device)}
-    for _ in range(args.warmup):
-        run_step(inp, out)
+    for dp in fresh_gradients(inp, args.warmup):
+        run_step(inp, out, dp)
+    grads = fresh_gradients(inp, args.steps)
     torch.cuda.synchronize()
     # Timed region: exactly `steps` steps, synchronised on both sides.
     t0 = time.perf_counter()
-    for _ in range(args.steps):
-        run_step(inp, out)
+    for dp in grads:
+        run_step(inp, out, dp)
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
     # Per-region HIP-event times over separate steps (not part of the timed region).
     timer = Timer()
-    for _ in range(args.steps):
-        run_step(inp, out, timer)
+    grads = fresh_gradients(inp, args.steps)
+    for dp in grads:
+        run_step(inp, out, dp, timer)
     torch.cuda.synchronize()
+    del grads
     flops = flops_step(m)
     regions = {}
     for name, f in flops.items():
@@ -200,19 +217,22 @@ def bench_gpu(args):
         kernels[name] = {"ms": round(ms, 4), "tflops": round(f / ms / 1e9, 1),
                          "pct_peak": round(100 * f / ms / 1e9 / PEAK_BF16_TFLOPS, 2),
                          "flops": f}
-    # RMSNorm statistics pass (HBM-bound part of qkv_fwd): one read of x, one rstd write.
-    from ops import _hip
+    # The RMSNorm row pass of qkv_fwd (HBM-bound): x read once, the normalized rows y and
+    # rstd written. The eager standalone forward launches the same kernel
+    # (rmsnorm_rows_reg_kernel) as rmsnorm_gate_mm's row pass.
+    from ops.activation_execution import bf16_rmsnorm
 
     rt = Timer()
     for _ in range(args.steps):
-        with rt.region("rstd"):
-            _hip.call("ws_rms_rstd", inp["qkv_x"].data_ptr(), D, out["rstd"].data_ptr(), m, D,
-                      float(inp["qkv_eps"]), _hip.stream(inp["qkv_x"]))
+        with rt.region("rows"):
+            bf16_rmsnorm(inp["qkv_x"], inp["qkv_norm_weight"], float(inp["qkv_eps"]), True)
     torch.cuda.synchronize()
-    rstd_ms = rt.mean_ms("rstd")
-    rstd_bytes = m * D * 2 + m * 4
-    hbm = {"rms_rstd": {"ms": round(rstd_ms, 4), "bytes": rstd_bytes,
-                        "gbs": round(rstd_bytes / rstd_ms / 1e6, 1)}}
+    rows_ms = rt.mean_ms("rows")
+    rows_bytes = 2 * m * D * 2 + m * 4 + D * 4
+    hbm = {"rmsnorm_rows": {"ms": round(rows_ms, 4), "bytes": rows_bytes,
+                            "gbs": round(rows_bytes / rows_ms / 1e6, 1),
+                            "frac_hbm": round(rows_bytes / rows_ms / 1e6 / PEAK_HBM_GBS, 4),
+                            "kernel": "rmsnorm_rows_reg_kernel<4> (qkv_fwd row pass)"}}
     # RMSNorm backward of the step (dX and the weight gradient, both launches): x and the
     # incoming gradient read, dX written, rstd read and the FP32 weight gradient written
     # once each (the per-block partials are not counted).
@@ -283,14 +303,17 @@ def bench_extra(args, device):
     dh = torch.empty((M, D), dtype=torch.bfloat16, device=device)
     one = torch.ones((), device=device)
     f5 = 4 * M * D * VOCAB
-    # Two variants: logits only in registers (the backward recomputes them with a GEMM),
-    # and logits stored by the forward (1 GiB of BF16) and read by the backward.
-    for key, store, note in (
-            ("config5_lm_head_ce_16384x2048x32768", False,
-             "logits fwd + dHidden; the backward's logit recompute is not counted"),
-            ("config5_lm_head_ce_stored_logits_16384x2048x32768", True,
-             "logits fwd + dHidden; the forward stores the BF16 logits, the backward reads them")):
-        state = CrossEntropyState(M, VOCAB, device, store_logits=store)
+    # Config 5 is the one-pass fused loss: each 8192-row chunk's BF16 logits exist only in
+    # the chunk workspace (512 MiB; the full [16384, 32768] logits never do), and the
+    # chunk's dHidden is formed while they are there; the backward scales by the upstream
+    # gradient. The two-pass variant (logits only in registers, recomputed by the
+    # backward) is timed beside it.
+    for key, fused, note in (
+            ("config5_lm_head_ce_16384x2048x32768", True,
+             "logits fwd + dHidden, one pass (ws_linear_ce_fused) + upstream scale"),
+            ("config5_two_pass_recompute_16384x2048x32768", False,
+             "logits fwd + dHidden; the backward recomputes the logits GEMM (not counted)")):
+        state = CrossEntropyState(M, VOCAB, device, d=D, fused=fused)
         for _ in range(args.warmup):
             linear_cross_entropy_forward(hidden, weight, targets, state)
             linear_cross_entropy_backward(hidden, weight, targets, state, one, out=dh)
@@ -306,8 +329,68 @@ def bench_extra(args, device):
             "ms": round(ms, 4), "fwd_ms": round(t.mean_ms("fwd"), 4),
             "bwd_ms": round(t.mean_ms("bwd"), 4), "tflops": round(f5 / ms / 1e9, 1),
             "pct_peak": round(100 * f5 / ms / 1e9 / PEAK_BF16_TFLOPS, 2), "flops_note": note}
-        del state
+        if fused:
+            fused_state = state
+        else:
+            del state
+    res["_hbm"] = lm_head_hbm_parts(args, fused_state, targets, device)
+    del fused_state
     return res
+
+
+def lm_head_hbm_parts(args, state, targets, device):
+    """The LM-head loss's HBM-bound passes at config 5, each timed alone with HIP events:
+    the row combine + mean (part_max / part_sum / target logit / targets read, lse and loss
+    written, then loss and targets read again), and the elementwise logit-gradient pass over
+    one 8192-row chunk, in place (BF16 logits read and gradients written)."""
+    from ops import _hip
+
+    parts = state.part_max.shape[1]
+    stream = _hip.stream(targets)
+    scale = torch.full((1,), 1.0 / M, device=device)
+    chunk = torch.empty((8192, VOCAB), dtype=torch.bfloat16, device=device).normal_()
+
+    def combine():
+        _hip.call("ws_linear_ce_combine", state.part_max.data_ptr(), state.part_sum.data_ptr(),
+                  state.target_logit.data_ptr(), targets.data_ptr(), state.lse.data_ptr(),
+                  state.loss.data_ptr(), state.mean.data_ptr(), state.count.data_ptr(), M,
+                  VOCAB, stream)
+
+    def logit_grad():
+        _hip.call("ws_linear_ce_logit_grad", chunk.data_ptr(), VOCAB, targets.data_ptr(),
+                  state.lse.data_ptr(), scale.data_ptr(), chunk.data_ptr(), VOCAB, 8192, VOCAB,
+                  stream)
+
+    out = {}
+    for name, fn, nbytes, kernels in (
+            ("ce_combine_mean", combine, M * (2 * parts * 4 + 4 + 8 + 4 + 4) + M * (4 + 8),
+             "ce_combine_kernel + ce_mean_kernel"),
+            ("ce_logit_grad_chunk", logit_grad, 2 * 8192 * VOCAB * 2 + 8192 * (8 + 4),
+             "ce_grad_logits_kernel, 8192 x 32768 in place")):
+        for _ in range(args.warmup):
+            fn()
+        t = Timer()
+        for _ in range(args.steps):
+            with t.region(name):
+                fn()
+        torch.cuda.synchronize()
+        ms = t.mean_ms(name)
+        out[name] = {"ms": round(ms, 4), "bytes": nbytes, "gbs": round(nbytes / ms / 1e6, 1),
+                     "frac_hbm": round(nbytes / ms / 1e6 / PEAK_HBM_GBS, 4),
+                     "kernel": kernels}
+    del chunk
+    return out
+
+
+def cpu_model() -> str:
+    """The host CPU's model name from /proc/cpuinfo (the platform string if absent)."""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
 
 
 def cpu_baseline(rows):
@@ -350,17 +433,27 @@ def cpu_baseline(rows):
 TRAFFIC_PROFILE = ROOT / "profiles" / "hbm_traffic_layer_step_m16384.md"
 
 
+TRACE_PROFILE = ROOT / "profiles" / "gemm_kernels_layer_step_m16384.md"
+
+
+def _profile_value(path: Path, tag: str, region: str):
+    """The number recorded on a ``<tag> <region> <value>`` line of a committed profile
+    summary, or None."""
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        parts = line.split()
+        if len(parts) == 3 and parts[0] == tag and parts[1] == region:
+            return float(parts[2])
+    return None
+
+
 def measured_traffic(region: str):
     """HBM bytes per launch of a bench region, measured with rocprofv3 FETCH_SIZE and
     WRITE_SIZE (scaled by a plain copy's readings) and recorded in the traffic profile;
     None when the region has no measurement there."""
-    if not TRAFFIC_PROFILE.exists():
-        return None
-    for line in TRAFFIC_PROFILE.read_text().splitlines():
-        parts = line.split()
-        if len(parts) == 3 and parts[0] == "traffic_bytes" and parts[1] == region:
-            return int(parts[2])
-    return None
+    value = _profile_value(TRAFFIC_PROFILE, "traffic_bytes", region)
+    return None if value is None else int(value)
 
 
 def main():
@@ -379,6 +472,7 @@ def main():
     torch.cuda.empty_cache()
     per_config = {} if args.no_extra else bench_extra(args, device)
     if not args.no_extra:
+        hbm.update(per_config.pop("_hbm"))
         hbm["attention_bwd_layout_4x16x32x128x64"] = bench_layout(args, device)
     value = step_flops / wall_ms / 1e9
     dom_name = max(kernels, key=lambda k: kernels[k]["ms"])
@@ -388,14 +482,22 @@ def main():
                 "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                 "frac": round(dom["flops"] / dom["ms"] / 1e9 / PEAK_BF16_TFLOPS, 4),
                 "traffic": measured_traffic(dom_name)}
+    # The same region's kernels in the committed rocprofv3 trace (sum of their average
+    # durations), for comparison with the HIP-event figure above.
+    trace_us = _profile_value(TRACE_PROFILE, "trace_us", dom_name)
+    if trace_us:
+        roofline["trace_us"] = trace_us
+        roofline["trace_achieved"] = round(dom["flops"] / trace_us / 1e6, 1)
+        roofline["trace_frac"] = round(dom["flops"] / trace_us / 1e6 / PEAK_BF16_TFLOPS, 4)
     cpu = None
     if not args.no_cpu:
         tflops, sec, threads = cpu_baseline(args.cpu_rows)
         cpu = {"value": round(tflops, 4), "unit": "TFLOP/s", "cores": threads,
                "kind": "port",
                "sample": f"the same step at M={args.cpu_rows} tokens (of {args.rows}), "
-                         f"median of >=3 runs, {sec:.2f} s/step, "
-                         f"CPU '{platform.processor() or platform.machine()}'"}
+                         f"median of >=3 runs, {sec:.2f} s/step",
+               "cpu_model": cpu_model(), "os_cpu_count": os.cpu_count(),
+               "torch_threads": threads}
     line = {"metric": METRIC, "value": round(value, 1), "unit": "TFLOP/s", "n_gpus": 1,
             "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(wall_ms, 4),
             "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",

@@ -251,6 +251,63 @@ int ws_linear_ce_backward(const void* hidden, int64_t ld_hidden, const void* wei
                           int64_t ld_dweight, const void* logits, void* stream);
 
 /*
+ * Fused LM-head cross-entropy in one pass: the outputs of ws_linear_ce_forward plus the
+ * gradients for a unit upstream gradient of the mean, dhidden [rows, d] BF16 and (nullable)
+ * dweight [vocab, d] FP32 (+=), with the numerics of ws_linear_ce_backward at grad_mean = 1.
+ * Rows go chunk_rows at a time through the workspace of ws_linear_ce_workspace_bytes: the
+ * chunk's logits GEMM stores its BF16 logits in the workspace chunk (the whole [rows, vocab]
+ * logits never exist), the chunk's row statistics give its lse and loss, one elementwise
+ * pass turns the stored logits into the logit gradients in place, and they feed the
+ * chunk's dHidden and head-weight GEMMs: one logits GEMM per row instead of the forward's
+ * and the backward's. `weight_t` as in ws_linear_ce_backward. Restates
+ * warpstate/model.py:316-334 with its autograd.
+ */
+int ws_linear_ce_fused(const void* hidden, int64_t ld_hidden, const void* weight,
+                       int64_t ld_weight, const void* weight_t, const int64_t* targets,
+                       int64_t rows, int64_t vocab, int64_t d, float* part_max, float* part_sum,
+                       float* target_logit, float* lse, float* loss, float* mean, int64_t* count,
+                       void* workspace, int64_t chunk_rows, void* dhidden, int64_t ld_dhidden,
+                       float* dweight, int64_t ld_dweight, void* stream);
+
+/*
+ * Backward of ws_linear_ce_fused for the actual upstream gradient grad_mean (device FP32
+ * scalar): dhidden [rows, d] BF16 (row stride ld_dhidden) and, when given, dweight
+ * [vocab, d] FP32 (contiguous, +=). When grad_mean is a power of two, scaling commutes with
+ * every rounding, and the results are grad_mean * dhidden_unit and dweight + grad_mean *
+ * dweight_unit: the two-pass backward's results bit for bit (dweight up to summation order
+ * into a nonzero buffer). Otherwise it runs the two-pass backward (ws_linear_ce_backward's
+ * arguments). The choice is made on the device, without a host synchronisation: both paths
+ * are launched and the kernels of the one not taken exit at once.
+ */
+int ws_linear_ce_fused_backward(const void* hidden, int64_t ld_hidden, const void* weight,
+                                int64_t ld_weight, const void* weight_t, const int64_t* targets,
+                                const float* lse, const int64_t* count, const float* grad_mean,
+                                int64_t rows, int64_t vocab, int64_t d, void* workspace,
+                                int64_t chunk_rows, const void* dhidden_unit, int64_t ld_unit,
+                                const float* dweight_unit, void* dhidden, int64_t ld_dhidden,
+                                float* dweight, void* stream);
+
+/*
+ * The second phase of ws_linear_ce_forward on its own: lse and loss per row from the
+ * statistics partials part_max / part_sum ([rows, ws_linear_ce_parts(vocab)]) and the
+ * target logits, then mean = sum(loss) / max(1, count) and the int64 count (the combine
+ * step of the chunked head, warpstate/model.py:326-334, ops/loss_experiment.py:18-19).
+ */
+int ws_linear_ce_combine(const float* part_max, const float* part_sum, const float* target_logit,
+                         const int64_t* targets, float* lse, float* loss, float* mean,
+                         int64_t* count, int64_t rows, int64_t vocab, void* stream);
+
+/*
+ * Logit gradients from BF16 logits: out = r(scale (exp(l - lse) - onehot)), zero rows for
+ * ignored targets, `scale` a device FP32 scalar; `out` may be `logits` (in place). vocab % 4
+ * == 0, row strides multiples of 8, 16-byte aligned buffers. The elementwise pass of the
+ * fused loss (autograd of F.cross_entropy on BF16 logits, warpstate/model.py:328-334).
+ */
+int ws_linear_ce_logit_grad(const void* logits, int64_t ld_logits, const int64_t* targets,
+                            const float* lse, const float* scale, void* out, int64_t ld_out,
+                            int64_t rows, int64_t vocab, void* stream);
+
+/*
  * Packed attention-backward gradient layout: out [B, N*C, 5*H*D] BF16 (token-major rows of
  * [q | k | v | gate | u], each H*D wide) from the saved head-major [B, N, H, C, D] BF16
  * tensors q_memory, q_local, tanh_k, k_local, v_local, memory, local, gate, u_write, tanh_u,

@@ -287,12 +287,12 @@ def test_fused_adapter_matches_unpatched_model(size, hip_calls):
         expected = reference(inputs, labels, return_logits=False)[1]
         hip_calls.clear()
         result = actual(inputs, labels, return_logits=False)[1]
-    for name in ("ws_rmsnorm_gate_mm", "ws_residual_mm", "ws_swiglu_mm", "ws_linear_ce_forward"):
+    for name in ("ws_rmsnorm_gate_mm", "ws_residual_mm", "ws_swiglu_mm", "ws_linear_ce_fused"):
         assert name in hip_calls, (name, hip_calls)
     expected.backward()
     hip_calls.clear()
     result.backward()
-    for name in ("ws_linear_ce_backward", "ws_sigmoid_backward_cols", "ws_swiglu_backward_mm",
+    for name in ("ws_linear_ce_fused_backward", "ws_sigmoid_backward_cols", "ws_swiglu_backward_mm",
                  "ws_mm_accumulate_f32", "ws_rmsnorm_backward"):
         assert any(call.startswith(name) for call in hip_calls), (name, hip_calls)
     assert math.isclose(result.item(), expected.item(), rel_tol=1e-3)

@@ -132,22 +132,25 @@ def test_config5_lm_head_cross_entropy_full():
     assert torch.count_nonzero(dh0).item() == 0
 
 
-def test_config5_stored_logits_match_the_recomputing_backward_bitwise():
-    """Config 5 with the logits kept by the forward (1 GiB of BF16): the backward's
-    elementwise logit gradients give the recomputing GEMM's dHidden bit for bit."""
+def test_config5_fused_and_stored_logits_match_the_recomputing_backward_bitwise():
+    """Config 5 three ways: the two-pass loss (logits only in registers, recomputed in the
+    backward), the one-pass fused loss (one 8192-row chunk of logits in the workspace at a
+    time) and the stored full logits (1 GiB of BF16). Loss and dHidden agree bit for bit
+    for a unit upstream gradient."""
     from ops.fused_execution import (CrossEntropyState, linear_cross_entropy_backward,
                                      linear_cross_entropy_forward)
 
     inp = cfg.lm_head_inputs(seed=0)
     hidden, weight, targets = (inp[k].cuda() for k in ("hidden", "weight", "targets"))
-    grad = torch.full((), 0.75, device="cuda")
+    grad = torch.ones((), device="cuda")
     got = []
-    for store in (False, True):
-        state = CrossEntropyState(hidden.shape[0], weight.shape[0], hidden.device,
-                                  store_logits=store)
+    for mode in ({}, {"fused": True, "d": 2048}, {"store_logits": True}):
+        state = CrossEntropyState(hidden.shape[0], weight.shape[0], hidden.device, **mode)
         linear_cross_entropy_forward(hidden, weight, targets, state)
         got.append((state, linear_cross_entropy_backward(hidden, weight, targets, state, grad)))
-    torch.cuda.synchronize()
-    (a, dha), (b, dhb) = got
-    assert torch.equal(a.loss, b.loss) and torch.equal(a.lse, b.lse)
-    assert torch.equal(dha, dhb)
+        torch.cuda.synchronize()
+    (a, dha), *others = got
+    for b, dhb in others:
+        assert torch.equal(a.loss, b.loss) and torch.equal(a.lse, b.lse)
+        assert torch.equal(a.mean, b.mean) and torch.equal(a.count, b.count)
+        assert torch.equal(dha, dhb)

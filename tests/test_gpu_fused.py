@@ -517,3 +517,87 @@ def test_rmsnorm_gate_projection_backward(m, d, n, gate, in_place):
     assert_bf16_close(dx, want_dx, "dx")
     assert rel_l2(dnw, want_dnw) <= 3e-3
     assert_f32_close(g.cpu(), want_g, "W_in gradient")
+
+
+@pytest.mark.parametrize("rows,d,vocab,chunk", [(512, 256, 1024, 256), (3000, 384, 2052, 1024),
+                                                (700, 136, 1030, 512)])
+def test_fused_cross_entropy_matches_the_two_pass_backward(rows, d, vocab, chunk):
+    """The one-pass fused loss (chunk logits kept in the workspace, gradients formed while
+    they are there) gives, for a unit upstream gradient, the two-pass loss, dHidden and
+    head-weight gradient bit for bit; another upstream gradient scales them. Shapes cover a
+    last 4-column piece (2052) and a vocabulary the stored-logits epilogue cannot take (1030,
+    which recomputes the chunk's logits)."""
+    from ops.fused_execution import (CrossEntropyState, linear_cross_entropy_backward,
+                                     linear_cross_entropy_forward)
+
+    gen = _gen(405)
+    h = torch.randn(rows, d, generator=gen).bfloat16()
+    w = (torch.randn(vocab, d, generator=gen) * 0.05).bfloat16()
+    t = torch.randint(0, vocab, (rows,), generator=gen)
+    t[::5] = -100
+    hc, wc, tc = h.cuda(), w.cuda(), t.cuda()
+    for g in (1.0, 0.25, 0.75):
+        grad = torch.full((), g, device="cuda")
+        got = []
+        for fused in (False, True):
+            state = CrossEntropyState(rows, vocab, hc.device, chunk_rows=chunk, d=d,
+                                      fused=fused, weight_grad=fused)
+            linear_cross_entropy_forward(hc, wc, tc, state)
+            # Bit-exact comparisons start from zero (the fused pass adds its chunk sum to
+            # the buffer at the end, the two-pass backward chunk by chunk).
+            gw = torch.full((vocab, d), 0.0 if g != 0.75 else 0.5, device="cuda")
+            dh = linear_cross_entropy_backward(hc, wc, tc, state, grad, weight_grad=gw)
+            got.append((state, dh, gw))
+        torch.cuda.synchronize()
+        (a, dha, gwa), (b, dhb, gwb) = got
+        for name in ("loss", "lse", "mean", "count"):
+            assert torch.equal(getattr(a, name), getattr(b, name)), name
+        # A power-of-two upstream gradient scales the unit gradients exactly; 0.75 runs the
+        # two-pass backward (chosen on the device) and so matches it exactly too.
+        assert torch.equal(dha, dhb)
+        if g != 0.75:
+            assert torch.equal(gwa, gwb)
+        else:
+            assert_f32_close(gwb.cpu(), gwa.cpu(), "fused dW, upstream 0.75")
+    want_loss, _mean, count, want_dh = oracle.linear_cross_entropy(h, w, t)
+    assert int(b.count.item()) == count
+    assert_f32_close(b.loss.cpu(), want_loss, "fused per-token loss")
+
+
+def test_cross_entropy_combine_and_logit_gradient_entry_points():
+    """ws_linear_ce_combine recomputes the forward's second phase from its partials (same
+    bits); ws_linear_ce_logit_grad turns BF16 logits into the oracle's logit gradients."""
+    from ops import _hip
+    from ops.fused_execution import CrossEntropyState, linear_cross_entropy_forward
+
+    rows, d, vocab = 640, 256, 2048
+    gen = _gen(406)
+    h = torch.randn(rows, d, generator=gen).bfloat16()
+    w = (torch.randn(vocab, d, generator=gen) * 0.05).bfloat16()
+    t = torch.randint(0, vocab, (rows,), generator=gen)
+    t[::9] = -100
+    hc, wc, tc = h.cuda(), w.cuda(), t.cuda()
+    state = linear_cross_entropy_forward(hc, wc, tc)
+    again = CrossEntropyState(rows, vocab, hc.device)
+    _hip.call("ws_linear_ce_combine", state.part_max.data_ptr(), state.part_sum.data_ptr(),
+              state.target_logit.data_ptr(), tc.data_ptr(), again.lse.data_ptr(),
+              again.loss.data_ptr(), again.mean.data_ptr(), again.count.data_ptr(), rows, vocab,
+              _hip.stream(hc))
+    logits = oracle.mm(h, w.T)
+    count = int(t.ne(-100).sum())
+    scale = torch.full((1,), 0.5 / count, device="cuda")
+    out = torch.empty(rows, vocab, dtype=torch.bfloat16, device="cuda")
+    gl = logits.cuda()
+    _hip.call("ws_linear_ce_logit_grad", gl.data_ptr(), vocab, tc.data_ptr(),
+              state.lse.data_ptr(), scale.data_ptr(), out.data_ptr(), vocab, rows, vocab,
+              _hip.stream(hc))
+    torch.cuda.synchronize()
+    for name in ("lse", "loss", "mean", "count"):
+        assert torch.equal(getattr(state, name), getattr(again, name)), name
+    soft = torch.softmax(logits.float(), dim=-1)
+    onehot = torch.zeros_like(soft)
+    valid = t.ne(-100)
+    onehot[valid.nonzero().squeeze(1), t[valid]] = 1.0
+    want = ((soft - onehot) * (0.5 / count) * valid.unsqueeze(1)).bfloat16()
+    assert_bf16_close(out, want, "logit gradients")
+    assert torch.count_nonzero(out.cpu()[~valid]).item() == 0

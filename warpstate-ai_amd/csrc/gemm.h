@@ -79,6 +79,9 @@ struct GemmParams {
   float* part_max; float* part_sum; float* tgt_logit; int parts_per_row;
   const float* grad_scale;  // device scalar: d(mean) / max(1, count)
   int row_offset;
+  // Device flag (nullable): when set, every workgroup exits at once. Lets a path whose need
+  // is decided on the device (the LM head's exact-scaling check) be launched unconditionally.
+  const int* skip_if;
   // Balanced FP32 accumulation (fast kernel): tiles [0, dp_tiles) of the raster run whole
   // and accumulate into g; the k-tiles of the other sk_tiles tiles (sk_units = sk_tiles x
   // k_tiles in all) are shared evenly by the gridDim.x workgroups, each piece writing a
@@ -673,6 +676,7 @@ gemm_kernel(const GemmParams p) {
   static_assert(!PAIRED || (FN % 2 == 0), "paired tiles need up/gate block pairs");
 
   extern __shared__ __attribute__((aligned(16))) unsigned short smem[];
+  if (p.skip_if != nullptr && *p.skip_if != 0) return;  // uniform: the whole grid exits
   unsigned short* lds_a = smem;                    // [2][BM * BK]
   unsigned short* lds_b = smem + 2 * BM * kBK;     // [2][BN * BK]
 

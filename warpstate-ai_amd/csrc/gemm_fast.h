@@ -610,6 +610,7 @@ __global__ void __launch_bounds__(kFNT) gemm_fast_kernel(const GemmParams p) {
   constexpr bool kMidIssue = AMODE == kMNContig || BMODE == kMNContig;
 
   extern __shared__ __attribute__((aligned(1024))) unsigned char fsmem[];
+  if (p.skip_if != nullptr && *p.skip_if != 0) return;  // uniform: the whole grid exits
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);

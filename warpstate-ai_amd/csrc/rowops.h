@@ -410,6 +410,74 @@ static __global__ void __launch_bounds__(1024) ce_mean_kernel(const float* __res
   }
 }
 
+// The valid-token count of the whole batch and the unit-upstream-gradient scale
+// 1 / max(1, count), before any chunk of the fused pass forms its gradients. One block.
+static __global__ void __launch_bounds__(1024) ce_count_kernel(const long* __restrict__ targets,
+                                                        int rows, long* __restrict__ count_out,
+                                                        float* __restrict__ scale) {
+  __shared__ long scnt[1024];
+  long c = 0;
+  for (int i = threadIdx.x; i < rows; i += 1024) c += targets[i] != -100 ? 1 : 0;
+  scnt[threadIdx.x] = c;
+  __syncthreads();
+  for (int stride = 512; stride > 0; stride >>= 1) {
+    if (threadIdx.x < stride) scnt[threadIdx.x] += scnt[threadIdx.x + stride];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    count_out[0] = scnt[0];
+    scale[0] = 1.0f / (float)(scnt[0] > 1 ? scnt[0] : 1);
+  }
+}
+
+// out = r(g * f32(in)) elementwise over [rows, d] BF16 (row strides ld_in, ld_out); runs
+// only when run_if (nullable) is set. With `vec` (d, ld_in, ld_out multiples of 8, 16-byte
+// aligned rows) each thread moves 8 elements as 16-byte vectors.
+static __global__ void __launch_bounds__(256) scale_bf16_rows_kernel(
+    const float* __restrict__ g, const unsigned short* __restrict__ in, long ld_in,
+    unsigned short* __restrict__ out, long ld_out, int rows, int d, int vec,
+    const int* __restrict__ run_if) {
+  if (run_if != nullptr && *run_if == 0) return;
+  const float scale = *g;
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (vec) {
+    const int per_row = d / 8;
+    if (i >= (long)rows * per_row) return;
+    const long r = i / per_row, c = (i - r * per_row) * 8;
+    const u32x4_t v = *reinterpret_cast<const u32x4_t*>(in + r * ld_in + c);
+    u32x4_t o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = pack_bf16x2(scale * lo_bf16(v[e]), scale * hi_bf16(v[e]));
+    *reinterpret_cast<u32x4_t*>(out + r * ld_out + c) = o;
+    return;
+  }
+  if (i >= (long)rows * d) return;
+  const long r = i / d, c = i - r * d;
+  out[r * ld_out + c] = to_bf16_bits(scale * bf16_bits_to_f32(in[r * ld_in + c]));
+}
+
+// acc += g * x elementwise over n FP32 values.
+static __global__ void __launch_bounds__(256) scale_add_f32_kernel(const float* __restrict__ g,
+                                                             const float* __restrict__ x,
+                                                             float* __restrict__ acc, long n,
+                                                             const int* __restrict__ run_if) {
+  if (run_if != nullptr && *run_if == 0) return;
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) acc[i] += *g * x[i];
+}
+
+// exact[0] = 1 when g is a positive or negative power of two (a normal FP32 number with an
+// all-zero mantissa): scaling by g then commutes with every BF16 and FP32 rounding of the
+// LM-head gradients, so the fused pass's unit gradients scaled by g are the gradients the
+// two-pass backward computes for g, bit for bit.
+static __global__ void ce_exact_scale_kernel(const float* __restrict__ g, int* __restrict__ exact) {
+  if (threadIdx.x == 0) {
+    const unsigned bits = __float_as_uint(g[0]);
+    const unsigned expo = (bits >> 23) & 0xff;
+    exact[0] = (bits & 0x7fffff) == 0 && expo != 0 && expo != 0xff;
+  }
+}
+
 // Backward scale of the summed cross-entropy: dmean / max(1, count).
 static __global__ void ce_scale_kernel(const float* __restrict__ dmean, const long* __restrict__ count,
                                 float* __restrict__ scale) {
@@ -451,7 +519,9 @@ static __global__ void __launch_bounds__(256) splitk_accum_kernel(const float* _
 static __global__ void __launch_bounds__(256) splitk_bf16_kernel(const float* __restrict__ part,
                                                           int splits, long split_stride,
                                                           unsigned short* __restrict__ out,
-                                                          long ldo, int M, int N) {
+                                                          long ldo, int M, int N,
+                                                          const int* __restrict__ skip_if) {
+  if (skip_if != nullptr && *skip_if != 0) return;
   long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
   long total = (long)M * N;
   if (i >= total) return;
@@ -569,10 +639,11 @@ namespace ws {
 // LM-head pass 2 epilogue: g = r(scale * exp(l - lse) - [n == target] scale), scale = 0 for
 // ignored rows (target -100). Thread (row, 8-column piece) reads and writes 16 bytes;
 // vocab % 4 == 0, a last half piece moves 8 bytes.
+// `g` may be `logits` itself (in place): each thread reads its 16 bytes before writing them.
 static __global__ void __launch_bounds__(256) ce_grad_logits_kernel(
-    const unsigned short* __restrict__ logits, long ld_logits, const long* __restrict__ targets,
+    const unsigned short* logits, long ld_logits, const long* __restrict__ targets,
     const float* __restrict__ lse, const float* __restrict__ grad_scale,
-    unsigned short* __restrict__ g, long ldg, int rows, int vocab) {
+    unsigned short* g, long ldg, int rows, int vocab) {
   const int per_row = (vocab + 2047) / 2048;  // blocks per row
   const int m = blockIdx.x / per_row;
   const int n = ((blockIdx.x % per_row) * 256 + threadIdx.x) * 8;

@@ -64,6 +64,17 @@ SIGNATURES = {
                                      _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64,
                                      _c_void_p, _i64, _c_void_p, _i64, _c_void_p, _i64,
                                      _c_void_p, _c_void_p]),
+    "ws_linear_ce_fused": (_i32, [_c_void_p, _i64, _c_void_p, _i64, _c_void_p, _c_void_p, _i64,
+                                  _i64, _i64, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+                                  _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _c_void_p,
+                                  _i64, _c_void_p, _i64, _c_void_p]),
+    "ws_linear_ce_fused_backward": (_i32, [_c_void_p, _i64, _c_void_p, _i64, _c_void_p,
+                                           _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64,
+                                           _i64, _i64, _c_void_p, _i64, _c_void_p, _i64,
+                                           _c_void_p, _c_void_p, _i64, _c_void_p, _c_void_p]),
+    "ws_linear_ce_combine": (_i32, [_c_void_p] * 8 + [_i64, _i64, _c_void_p]),
+    "ws_linear_ce_logit_grad": (_i32, [_c_void_p, _i64, _c_void_p, _c_void_p, _c_void_p,
+                                       _c_void_p, _i64, _i64, _i64, _c_void_p]),
     "ws_backward_layout": (_i32, [_c_void_p] * 15 + [_i64] * 5 + [_f32, _i32, _c_void_p,
                                                                    _c_void_p, _c_void_p]),
 }

@@ -296,12 +296,25 @@ def mm_accumulate_group_(items, round_bf16: bool = True,
 
 
 class CrossEntropyState:
-    """Per-call buffers of the fused LM-head cross-entropy. With ``store_logits`` the
-    forward also keeps the BF16 logits ([rows, vocab], 2 bytes each) and the backward
-    reads them instead of recomputing the logits GEMM."""
+    """Per-call buffers of the fused LM-head cross-entropy, in one of three modes:
+
+    * default: the forward keeps only row statistics; the backward recomputes each chunk's
+      logits with a GEMM whose epilogue forms the logit gradients;
+    * ``fused``: the forward computes, chunk by chunk, the loss and the gradients for a
+      unit upstream gradient (``ws_linear_ce_fused``: one logits GEMM per row, whose BF16
+      logits live only in the one-chunk workspace); the backward scales them by the actual
+      upstream gradient. Needs ``d``; ``weight_grad`` also keeps the head weight's
+      unit gradient (FP32 [vocab, d]);
+    * ``store_logits``: the forward keeps the full BF16 logits ([rows, vocab]) and the
+      backward reads them instead of recomputing the logits GEMM.
+    """
 
     def __init__(self, rows, vocab, device, chunk_rows=DEFAULT_CE_CHUNK_ROWS, d=None,
-                 store_logits=False):
+                 store_logits=False, fused=False, weight_grad=False):
+        if fused and store_logits:
+            raise ValueError("A cross-entropy state is either fused or stores the logits")
+        if fused and d is None:
+            raise ValueError("A fused cross-entropy state needs the hidden width d")
         parts = _hip.query("ws_linear_ce_parts", vocab)
         f32 = dict(dtype=torch.float32, device=device)
         self.part_max = torch.empty((rows, parts), **f32)
@@ -311,16 +324,21 @@ class CrossEntropyState:
         self.loss = torch.empty((rows,), **f32)
         self.mean = torch.empty((), **f32)
         self.count = torch.empty((), dtype=torch.int64, device=device)
-        self.rows, self.vocab = rows, vocab
+        self.rows, self.vocab, self.d = rows, vocab, d
         self.chunk_rows = min(chunk_rows, rows)
         self.logits = (torch.empty((rows, vocab), dtype=torch.bfloat16, device=device)
                        if store_logits else None)
+        self.fused = fused
+        self.dhidden_unit = (torch.empty((rows, d), dtype=torch.bfloat16, device=device)
+                             if fused else None)
+        self.dweight_unit = (torch.empty((vocab, d), **f32) if fused and weight_grad else None)
+        self.weight_t = None
         self.workspace = None
         if d is not None:
             self.backward_workspace(d)
 
     def backward_workspace(self, d):
-        """The backward's workspace (scale, one chunk of BF16 logit gradients, split-K
+        """The chunk workspace (scale, one chunk of BF16 logits / logit gradients, split-K
         partials), allocated once per hidden width; 256-byte aligned by the allocator."""
         need = _hip.query("ws_linear_ce_workspace_bytes", self.rows, self.vocab, d,
                           self.chunk_rows)
@@ -360,6 +378,12 @@ def _check_state(state: CrossEntropyState, rows: int, vocab: int, device) -> Non
         _check_buffer(buffer, shape, dtype, device, "state." + name)
     if state.logits is not None:
         _check_buffer(state.logits, (rows, vocab), torch.bfloat16, device, "state.logits")
+    if state.fused:
+        _check_buffer(state.dhidden_unit, (rows, state.d), torch.bfloat16, device,
+                      "state.dhidden_unit")
+        if state.dweight_unit is not None:
+            _check_buffer(state.dweight_unit, (vocab, state.d), torch.float32, device,
+                          "state.dweight_unit")
     if not 1 <= state.chunk_rows <= rows:
         raise ValueError("CrossEntropyState chunk_rows must lie in [1, rows]")
 
@@ -375,6 +399,26 @@ def linear_cross_entropy_forward(hidden: torch.Tensor, weight: torch.Tensor,
     if state is None:
         state = CrossEntropyState(rows, vocab, hidden.device)
     _check_state(state, rows, vocab, hidden.device)
+    if state.fused:
+        if state.d != d:
+            raise ValueError(f"The fused CrossEntropyState was built for d={state.d}, not {d}")
+        workspace = state.backward_workspace(d)
+        weight_t = transpose(weight) if rows >= TRANSPOSE_MIN_ROWS else None
+        # Kept for the backward's two-pass fallback (an upstream gradient that is not a
+        # power of two).
+        state.weight_t = weight_t
+        if state.dweight_unit is not None:
+            state.dweight_unit.zero_()
+        _hip.call("ws_linear_ce_fused", hidden.data_ptr(), hidden.stride(0), weight.data_ptr(),
+                  weight.stride(0), _hip.ptr(weight_t), targets.data_ptr(), rows, vocab, d,
+                  state.part_max.data_ptr(), state.part_sum.data_ptr(),
+                  state.target_logit.data_ptr(), state.lse.data_ptr(), state.loss.data_ptr(),
+                  state.mean.data_ptr(), state.count.data_ptr(), workspace.data_ptr(),
+                  state.chunk_rows, state.dhidden_unit.data_ptr(), state.dhidden_unit.stride(0),
+                  _hip.ptr(state.dweight_unit),
+                  0 if state.dweight_unit is None else state.dweight_unit.stride(0),
+                  _hip.stream(hidden))
+        return state
     _hip.call("ws_linear_ce_forward", hidden.data_ptr(), hidden.stride(0), weight.data_ptr(),
               weight.stride(0), targets.data_ptr(), rows, vocab, d, state.part_max.data_ptr(),
               state.part_sum.data_ptr(), state.target_logit.data_ptr(), state.lse.data_ptr(),
@@ -405,7 +449,20 @@ def linear_cross_entropy_backward(hidden: torch.Tensor, weight: torch.Tensor,
     _check_buffer(out, (rows, d), torch.bfloat16, hidden.device, "out", contiguous=False)
     if weight_grad is not None:
         _check_buffer(weight_grad, (vocab, d), torch.float32, hidden.device, "weight_grad",
-                      contiguous=False)
+                      contiguous=state.fused)
+    if state.fused:
+        if state.d != d:
+            raise ValueError(f"The fused CrossEntropyState was built for d={state.d}, not {d}")
+        if weight_grad is not None and state.dweight_unit is None:
+            raise ValueError("This fused CrossEntropyState was built without weight_grad")
+        _hip.call("ws_linear_ce_fused_backward", hidden.data_ptr(), hidden.stride(0),
+                  weight.data_ptr(), weight.stride(0), _hip.ptr(state.weight_t),
+                  targets.data_ptr(), state.lse.data_ptr(), state.count.data_ptr(),
+                  grad_mean.data_ptr(), rows, vocab, d, state.backward_workspace(d).data_ptr(),
+                  state.chunk_rows, state.dhidden_unit.data_ptr(), state.dhidden_unit.stride(0),
+                  None if weight_grad is None else state.dweight_unit.data_ptr(),
+                  out.data_ptr(), out.stride(0), _hip.ptr(weight_grad), _hip.stream(hidden))
+        return out
     workspace = state.backward_workspace(d)
     # The dHidden GEMM reads the head weight along the vocabulary: give it W^T rows.
     weight_t = transpose(weight) if rows >= TRANSPOSE_MIN_ROWS else None
@@ -439,7 +496,12 @@ class LinearCrossEntropy(torch.autograd.Function):
     @staticmethod
     def forward(ctx, hidden, weight, targets, chunk_rows=DEFAULT_CE_CHUNK_ROWS):
         h, w = _bf16_rows(hidden), _bf16_rows(weight)
-        state = CrossEntropyState(h.shape[0], w.shape[0], h.device, chunk_rows)
+        # With gradients to come, the fused pass computes them for a unit upstream gradient
+        # while it has each chunk's logits (one logits GEMM per row); the backward only
+        # scales them.
+        wants = ctx.needs_input_grad
+        state = CrossEntropyState(h.shape[0], w.shape[0], h.device, chunk_rows, d=h.shape[1],
+                                  fused=wants[0] or wants[1], weight_grad=wants[1])
         linear_cross_entropy_forward(h, w, targets, state)
         ctx.save_for_backward(h, w, targets)
         ctx.state = state
