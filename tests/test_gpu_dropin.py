@@ -254,7 +254,7 @@ def test_compiled_autograd_fused_projection_dx_dw_and_recomputation(algorithm, r
 
 # --- the fused training adapter ------------------------------------------------------------
 
-@pytest.mark.parametrize("size", ["tiny", "medium"])
+@pytest.mark.parametrize("size", ["tiny", "medium", "medium_checkpointed"])
 def test_fused_adapter_matches_unpatched_model(size, hip_calls):
     """apply_fused_execution routes norm1 -> in_proj -> gate sigmoid, the residual
     projections, the SwiGLU block and the chunked tied-head loss through the fused
@@ -269,7 +269,8 @@ def test_fused_adapter_matches_unpatched_model(size, hip_calls):
     else:
         vocab = 2048
         reference = _model(vocab_size=vocab, d_model=256, n_heads=4, n_cores=2,
-                           logical_depth=3, ffn_hidden=512, loss_chunk_size=96)
+                           logical_depth=3, ffn_hidden=512, loss_chunk_size=96,
+                           gradient_checkpointing=size == "medium_checkpointed")
         tokens = (4, 64)
     reference = reference.cuda()
     actual = copy.deepcopy(reference)

@@ -82,7 +82,12 @@ def test_layer_step_replays_bitwise_under_graph_capture():
             assert torch.equal(g, e), f"replay {replay}: weight gradient {i} differs"
 
 
-def test_lm_head_cross_entropy_replays_bitwise_under_graph_capture():
+@pytest.mark.parametrize("mode", ["two_pass", "fused"])
+def test_lm_head_cross_entropy_replays_bitwise_under_graph_capture(mode):
+    """The LM-head loss and its gradients captured once and replayed: every replay equals the
+    eager step bit for bit. For the fused loss the upstream gradient changes between replays
+    (1.0, 0.75, 1.0): the backward's choice between scaling the unit gradients and the
+    two-pass recompute is made on the device, so one captured graph serves both."""
     from ops.fused_execution import (CrossEntropyState, linear_cross_entropy_backward,
                                      linear_cross_entropy_forward)
 
@@ -95,7 +100,8 @@ def test_lm_head_cross_entropy_replays_bitwise_under_graph_capture():
     targets = targets.cuda()
     grad_mean = torch.ones((), device="cuda")
     wgrad0 = (torch.randn(vocab, d, generator=g) * 1e-4).cuda()
-    state = CrossEntropyState(rows, vocab, hidden.device, d=d)
+    fused = mode == "fused"
+    state = CrossEntropyState(rows, vocab, hidden.device, d=d, fused=fused, weight_grad=fused)
     dh = torch.empty(rows, d, dtype=torch.bfloat16, device="cuda")
     wgrad = wgrad0.clone()
 
@@ -104,22 +110,29 @@ def test_lm_head_cross_entropy_replays_bitwise_under_graph_capture():
         linear_cross_entropy_backward(hidden, weight, targets, state, grad_mean, out=dh,
                                       weight_grad=wgrad)
 
-    step()
-    torch.cuda.synchronize()
-    eager = [state.loss.clone(), state.lse.clone(), state.mean.clone(), state.count.clone(),
-             dh.clone(), wgrad.clone()]
+    grads = (1.0, 0.75, 1.0) if fused else (1.0, 1.0, 1.0)
+    eager = {}
+    for value in sorted(set(grads)):
+        grad_mean.fill_(value)
+        wgrad.copy_(wgrad0)
+        step()
+        torch.cuda.synchronize()
+        eager[value] = [state.loss.clone(), state.lse.clone(), state.mean.clone(),
+                        state.count.clone(), dh.clone(), wgrad.clone()]
     wgrad.copy_(wgrad0)
+    grad_mean.fill_(1.0)
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
         step()
     torch.cuda.synchronize()
-    for replay in range(3):
+    for replay, value in enumerate(grads):
         state.loss.zero_()
         dh.zero_()
         wgrad.copy_(wgrad0)
+        grad_mean.fill_(value)
         torch.cuda.synchronize()
         graph.replay()
         torch.cuda.synchronize()
         got = [state.loss, state.lse, state.mean, state.count, dh, wgrad]
-        for i, (o, e) in enumerate(zip(got, eager)):
-            assert torch.equal(o, e), f"replay {replay}: output {i} differs from the eager step"
+        for i, (o, e) in enumerate(zip(got, eager[value])):
+            assert torch.equal(o, e), f"replay {replay} (grad {value}): output {i} differs"
