@@ -21,7 +21,8 @@ configurations are timed beside it and reported under ``per_config``: config 1 (
 two-pass variant that keeps the logits only in registers and recomputes them). The
 HBM-bound passes (the RMSNorm row pass, the RMSNorm backward, the LM-head combine and
 logit-gradient passes, the attention-backward layout) are timed alone under
-``hbm_parts``.
+``hbm_parts``, each as back-to-back calls queued behind a spin kernel between one event
+pair, so the short kernels' time carries no host launch gaps.
 
 ``roofline`` describes the dominant kernel of the step (the FP32-accumulating wgrad GEMM
 of the MLP backward by default); its average launch time comes from HIP events around
@@ -104,6 +105,23 @@ class Timer:
 
     def reset(self):
         self.events = {}
+
+
+def queued_ms(fn, calls):
+    """Mean ms per call of ``calls`` back-to-back calls of ``fn`` between one HIP-event pair
+    on the current stream. A bounded spin kernel launched first keeps the GPU busy while the
+    host queues the calls, so host launch overhead opens no gaps between short kernels and
+    the figure is the kernels' own time (as a kernel trace reports it)."""
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda._sleep(10_000_000)
+    start.record()
+    for _ in range(calls):
+        fn()
+    end.record()
+    end.synchronize()
+    return start.elapsed_time(end) / calls
 
 
 def gpu_inputs(m, device):
@@ -222,12 +240,8 @@ def bench_gpu(args):
     # (rmsnorm_rows_reg_kernel) as rmsnorm_gate_mm's row pass.
     from ops.activation_execution import bf16_rmsnorm
 
-    rt = Timer()
-    for _ in range(args.steps):
-        with rt.region("rows"):
-            bf16_rmsnorm(inp["qkv_x"], inp["qkv_norm_weight"], float(inp["qkv_eps"]), True)
-    torch.cuda.synchronize()
-    rows_ms = rt.mean_ms("rows")
+    rows_ms = queued_ms(lambda: bf16_rmsnorm(inp["qkv_x"], inp["qkv_norm_weight"],
+                                             float(inp["qkv_eps"]), True), args.steps)
     rows_bytes = 2 * m * D * 2 + m * 4 + D * 4
     hbm = {"rmsnorm_rows": {"ms": round(rows_ms, 4), "bytes": rows_bytes,
                             "gbs": round(rows_bytes / rows_ms / 1e6, 1),
@@ -238,11 +252,8 @@ def bench_gpu(args):
     # once each (the per-block partials are not counted).
     from ops.activation_execution import _rms_backward
 
-    for _ in range(args.steps):
-        with rt.region("rms_bwd"):
-            _rms_backward(inp["qkv_x"], inp["qkv_norm_weight"], out["rstd"], out["qkv_z"], True)
-    torch.cuda.synchronize()
-    bwd_ms = rt.mean_ms("rms_bwd")
+    bwd_ms = queued_ms(lambda: _rms_backward(inp["qkv_x"], inp["qkv_norm_weight"], out["rstd"],
+                                             out["qkv_z"], True), args.steps)
     bwd_bytes = 3 * m * D * 2 + m * 4 + D * 4
     hbm["rmsnorm_backward"] = {"ms": round(bwd_ms, 4), "bytes": bwd_bytes,
                                "gbs": round(bwd_bytes / bwd_ms / 1e6, 1),
@@ -261,19 +272,16 @@ def bench_layout(args, device):
     out = torch.empty((b, n * c, 5 * h * d), dtype=torch.bfloat16, device=device)
     ops = {"single": prepare_layout(inputs, "single", output=out),
            "profile": prepare_layout(inputs, "profile", output=out)}
-    timer = Timer()
+    times = {}
     for name, operation in ops.items():
         for _ in range(args.warmup):
             operation()
-        for _ in range(args.steps):
-            with timer.region(name):
-                operation()
-    torch.cuda.synchronize()
+        times[name] = queued_ms(operation, args.steps)
     nbytes = 34 * inputs.q_memory.numel()
-    ms = timer.mean_ms("single")
+    ms = times["single"]
     return {"ms": round(ms, 4), "bytes": nbytes, "gbs": round(nbytes / ms / 1e6, 1),
             "frac_hbm": round(nbytes / ms / 1e6 / PEAK_HBM_GBS, 4),
-            "profile_baseline_ms": round(timer.mean_ms("profile"), 4)}
+            "profile_baseline_ms": round(times["profile"], 4)}
 
 
 def bench_extra(args, device):
@@ -339,7 +347,7 @@ def bench_extra(args, device):
 
 
 def lm_head_hbm_parts(args, state, targets, device):
-    """The LM-head loss's HBM-bound passes at config 5, each timed alone with HIP events:
+    """The LM-head loss's HBM-bound passes at config 5, each timed alone (``queued_ms``):
     the row combine + mean (part_max / part_sum / target logit / targets read, lse and loss
     written, then loss and targets read again), and the elementwise logit-gradient pass over
     one 8192-row chunk, in place (BF16 logits read and gradients written)."""
@@ -369,12 +377,7 @@ def lm_head_hbm_parts(args, state, targets, device):
              "ce_grad_logits_kernel, 8192 x 32768 in place")):
         for _ in range(args.warmup):
             fn()
-        t = Timer()
-        for _ in range(args.steps):
-            with t.region(name):
-                fn()
-        torch.cuda.synchronize()
-        ms = t.mean_ms(name)
+        ms = queued_ms(fn, args.steps)
         out[name] = {"ms": round(ms, 4), "bytes": nbytes, "gbs": round(nbytes / ms / 1e6, 1),
                      "frac_hbm": round(nbytes / ms / 1e6 / PEAK_HBM_GBS, 4),
                      "kernel": kernels}
