@@ -143,7 +143,8 @@ def gpu_inputs(m, device):
 
 
 def run_step(inp, out, dp, timer=None):
-    """One hot-path pass; every kernel launches through the C ABI on the current stream.
+    """One hot-path pass on the current stream: every kernel launches through the C ABI,
+    except the two plain input-gradient GEMMs, which run on hipBLASLt (``dgrad_mm``).
 
     ``dp`` is this step's incoming gradient of the input projection's output. The QKV
     backward applies the gate-sigmoid backward to it in place (rmsnorm_gate_mm_backward
@@ -152,8 +153,9 @@ def run_step(inp, out, dp, timer=None):
     from contextlib import nullcontext
 
     from ops.activation_execution import _rms_backward
-    from ops.fused_execution import (mm, mm_accumulate_, mm_accumulate_group_, residual_mm,
-                                     rmsnorm_gate_mm, sigmoid_backward_cols, swiglu_backward_mm)
+    from ops.fused_execution import (dgrad_mm, mm_accumulate_, mm_accumulate_group_,
+                                     residual_mm, rmsnorm_gate_mm, sigmoid_backward_cols,
+                                     swiglu_backward_mm)
     from ops.matmul_epilogue import launch_swiglu_mm
 
     reg = timer.region if timer else (lambda name: nullcontext())
@@ -170,7 +172,7 @@ def run_step(inp, out, dp, timer=None):
             dpacked = swiglu_backward_mm(inp["mlp_dy"], inp["mlp_w_down"], packed, True,
                                          out=out["dpacked"])
         with reg("mlp_bwd.dx"):
-            mm(dpacked, inp["mlp_w_upgate"])
+            dgrad_mm(dpacked, inp["mlp_w_upgate"])
         with reg("mlp_bwd.wgrad"):
             # W_down's and W_upgate's gradients in one launch (both reduce over tokens).
             mm_accumulate_group_([(inp["mlp_g_down"], inp["mlp_dy"].T, act),
@@ -181,7 +183,7 @@ def run_step(inp, out, dp, timer=None):
         # consumer, so the sigmoid backward rewrites its gate columns in place.
         dp = sigmoid_backward_cols(dp, out["qkv"], GATE, dp)
         with reg("qkv_bwd.dx"):
-            dy = mm(dp, inp["qkv_w"])
+            dy = dgrad_mm(dp, inp["qkv_w"])
         with reg("qkv_bwd.wgrad"):
             mm_accumulate_(inp["qkv_g"], dp.T, out["qkv_z"], True)
         _rms_backward(inp["qkv_x"], inp["qkv_norm_weight"], out["rstd"], dy, True)

@@ -334,6 +334,25 @@ def test_weight_gradient_zero_upstream_leaves_buffer_bitwise():
     assert torch.equal(g, before)
 
 
+@pytest.mark.parametrize("m,n,k", [(2048, 1536, 768), (100, 384, 200), (1100, 520, 264)])
+def test_input_gradient_gemm(m, n, k):
+    """dgrad_mm: r(grad @ W) with W [N, K] in nn.Linear layout (hipBLASLt on the
+    K-contiguous copy of W from 1024 rows on, on W as given below that)."""
+    from ops.fused_execution import dgrad_mm, mm
+
+    g = torch.Generator().manual_seed(m + n + k)
+    grad = torch.randn(m, n, generator=g).bfloat16()
+    w = (torch.randn(n, k, generator=g) * 0.05).bfloat16()
+    dx = dgrad_mm(grad.cuda(), w.cuda())
+    torch.cuda.synchronize()
+    want = oracle.mm(grad, w)
+    assert dx.shape == (m, k) and dx.dtype == torch.bfloat16
+    assert_bf16_close(dx, want, "dgrad_mm")
+    assert_bf16_close(mm(grad.cuda(), w.cuda()), want, "mm on the same operands")
+    with pytest.raises(ValueError):
+        dgrad_mm(grad.cuda(), w.cuda().T.contiguous())
+
+
 def test_mlp_backward_matches_oracle():
     from ops.fused_execution import mlp_backward
 

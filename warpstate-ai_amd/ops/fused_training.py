@@ -13,8 +13,8 @@ core and of the loss that the fused kernels of ``ops.fused_execution`` cover:
   cross-entropy (``linear_cross_entropy``), whose logits never reach HBM.
 
 The backward of each piece is one autograd function built from the fused backward kernels:
-the gate-sigmoid backward, dX GEMMs, the SwiGLU backward fused on the dAct GEMM, and the
-RMSNorm backward. The projection weights' gradients are accumulated straight into the FP32
+the gate-sigmoid backward, the SwiGLU backward fused on the dAct GEMM and the RMSNorm
+backward, with the plain input-gradient GEMMs on hipBLASLt (``dgrad_mm``). The projection weights' gradients are accumulated straight into the FP32
 masters' ``.grad`` with the FP32-accumulating GEMM, G += f32(r(dY^T X))
 (test_gradient_execution.py:243-246), in one grouped launch for the MLP's two weights;
 the function returns no gradient for them, so no BF16 weight gradient is materialised
@@ -67,7 +67,7 @@ class _NormProjection(torch.autograd.Function):
         from ops.activation_execution import _rms_backward
 
         dp = fx.sigmoid_backward_cols(dout.contiguous(), out, ctx.gate)
-        dy = fx.mm(dp, w)
+        dy = fx.dgrad_mm(dp, w)
         if ctx.needs_input_grad[2]:
             fx.mm_accumulate_(_grad_buffer(ctx.weight), dp.T, normed, True)
         dx, dnorm = _rms_backward(x, norm_weight, rstd, dy, True)
@@ -90,7 +90,7 @@ class _ResidualProjection(torch.autograd.Function):
         dout = dout.contiguous()
         if ctx.needs_input_grad[1]:
             fx.mm_accumulate_(_grad_buffer(ctx.weight), dout.T, a, True)
-        return fx.mm(dout, w) if ctx.needs_input_grad[0] else None, None, dout
+        return fx.dgrad_mm(dout, w) if ctx.needs_input_grad[0] else None, None, dout
 
 
 class _SwiGLUBlock(torch.autograd.Function):
@@ -120,7 +120,7 @@ class _SwiGLUBlock(torch.autograd.Function):
         if ctx.needs_input_grad[1]:
             groups.append((_grad_buffer(w_upgate), dpacked.T, h))
         fx.mm_accumulate_group_(groups, True)
-        dh = fx.mm(dpacked, wug) if ctx.needs_input_grad[0] else None
+        dh = fx.dgrad_mm(dpacked, wug) if ctx.needs_input_grad[0] else None
         return dh, None, None, dout
 
 
