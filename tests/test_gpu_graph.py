@@ -136,3 +136,30 @@ def test_lm_head_cross_entropy_replays_bitwise_under_graph_capture(mode):
         got = [state.loss, state.lse, state.mean, state.count, dh, wgrad]
         for i, (o, e) in enumerate(zip(got, eager[value])):
             assert torch.equal(o, e), f"replay {replay} (grad {value}): output {i} differs"
+
+
+@pytest.mark.parametrize("m,n,k", [(16384, 11264, 2048), (16384, 9216, 2048), (512, 768, 256)])
+def test_input_gradient_gemm_replays_bitwise_under_graph_capture(m, n, k):
+    """dgrad_mm (the weight transpose, then hipBLASLt) captured once at the layer's shapes
+    and replayed three times with other work and a cleared output between replays: every
+    replay equals the eager call bit for bit. hipBLASLt's stream-K kernel for these shapes
+    clears its workspace with a fill before each launch, which the graph records."""
+    from ops.fused_execution import dgrad_mm
+
+    g = torch.Generator().manual_seed(m + n)
+    grad = torch.randn(m, n, generator=g).bfloat16().cuda()
+    weight = (torch.randn(n, k, generator=g) * 0.05).bfloat16().cuda()
+    eager = dgrad_mm(grad, weight).clone()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = dgrad_mm(grad, weight)
+    torch.cuda.synchronize()
+    scratch = torch.randn(2048, 2048, device="cuda").bfloat16()
+    for replay in range(3):
+        out.zero_()
+        scratch = torch.mm(scratch, scratch.T.contiguous()) / 2048
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {replay} differs from the eager call"
