@@ -254,13 +254,37 @@ def test_compiled_autograd_fused_projection_dx_dw_and_recomputation(algorithm, r
 
 # --- the fused training adapter ------------------------------------------------------------
 
-@pytest.mark.parametrize("size", ["tiny", "medium", "medium_checkpointed"])
+def _compile_training_cores(model, backend):
+    """Each core's forward compiled whole (fullgraph) for training calls, as the reference's
+    compile_training_cores does (run_40b.py:430-438)."""
+    for core in model.cores:
+        eager = core.forward
+        compiled = torch.compile(eager, fullgraph=True, dynamic=False, backend=backend)
+
+        def forward(*args, _core=core, _eager=eager, _compiled=compiled, **kwargs):
+            fn = _compiled if _core.training and torch.is_grad_enabled() else _eager
+            return fn(*args, **kwargs)
+
+        core.forward = forward
+
+
+@pytest.mark.parametrize("size", ["tiny", "medium", "medium_checkpointed",
+                                  "medium_compiled_cores", "medium_compiled_model"])
 def test_fused_adapter_matches_unpatched_model(size, hip_calls):
     """apply_fused_execution routes norm1 -> in_proj -> gate sigmoid, the residual
     projections, the SwiGLU block and the chunked tied-head loss through the fused
     kernels; loss and every parameter gradient agree with the unpatched model under BF16
-    autocast with BF16 residuals, an AdamW step keeps FP32 state and the state dict is
-    untouched."""
+    autocast with BF16 residuals, the weight gradients reach autograd's hooks, an AdamW
+    step keeps FP32 state and the state dict is untouched. The compiled variants compile
+    the patched cores with fullgraph=True (the fused pieces are registered operators) or
+    the whole model (the loss then runs eagerly)."""
+    try:
+        _fused_adapter_case(size, hip_calls)
+    finally:
+        torch._dynamo.reset()
+
+
+def _fused_adapter_case(size, hip_calls):
     from ops.fused_training import apply_fused_execution
     from ops.residual_experiment import apply_bf16_residuals
 
@@ -279,6 +303,13 @@ def test_fused_adapter_matches_unpatched_model(size, hip_calls):
     apply_fused_execution(actual)
     for model in (reference, actual):
         apply_bf16_residuals(model)
+    run = actual
+    if size == "medium_compiled_cores":
+        _compile_training_cores(actual, "aot_eager")
+    elif size == "medium_compiled_model":
+        run = torch.compile(actual, backend="aot_eager")
+    hooked = []
+    actual.cores[0].in_proj.weight.register_hook(lambda g: hooked.append(g.dtype))
     gen = torch.Generator("cpu").manual_seed(11)
     inputs = torch.randint(vocab, tokens, generator=gen).cuda()
     labels = torch.randint(vocab, tokens, generator=gen)
@@ -287,12 +318,14 @@ def test_fused_adapter_matches_unpatched_model(size, hip_calls):
     with torch.autocast("cuda", dtype=torch.bfloat16):
         expected = reference(inputs, labels, return_logits=False)[1]
         hip_calls.clear()
-        result = actual(inputs, labels, return_logits=False)[1]
+        result = run(inputs, labels, return_logits=False)[1]
     for name in ("ws_rmsnorm_gate_mm", "ws_residual_mm", "ws_swiglu_mm", "ws_linear_ce_fused"):
         assert name in hip_calls, (name, hip_calls)
     expected.backward()
     hip_calls.clear()
     result.backward()
+    # The projection weight's gradient went through autograd (where DDP's hooks sit).
+    assert hooked and all(dtype == torch.float32 for dtype in hooked), hooked
     for name in ("ws_linear_ce_fused_backward", "ws_sigmoid_backward_cols", "ws_swiglu_backward_mm",
                  "ws_mm_accumulate_f32", "ws_rmsnorm_backward"):
         assert any(call.startswith(name) for call in hip_calls), (name, hip_calls)

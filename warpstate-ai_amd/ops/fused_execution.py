@@ -542,8 +542,10 @@ class LinearCrossEntropy(torch.autograd.Function):
                 weight_grad.to(weight_dtype) if want_w else None, None, None)
 
 
+@torch.compiler.disable
 def linear_cross_entropy(hidden, weight, targets, chunk_rows=DEFAULT_CE_CHUNK_ROWS):
-    """(mean, per-token loss) of the fused LM head, with autograd to hidden and weight."""
+    """(mean, per-token loss) of the fused LM head, with autograd to hidden and weight.
+    Under torch.compile it runs eagerly (a graph break), with its own buffers."""
     return LinearCrossEntropy.apply(hidden, weight, targets, chunk_rows)
 
 

@@ -12,15 +12,17 @@ core and of the loss that the fused kernels of ``ops.fused_execution`` cover:
 * the chunked tied-head loss (warpstate/model.py:316-334) becomes the fused
   cross-entropy (``linear_cross_entropy``), whose logits never reach HBM.
 
-The backward of each piece is one autograd function built from the fused backward kernels:
-the gate-sigmoid backward, the SwiGLU backward fused on the dAct GEMM and the RMSNorm
-backward, with the plain input-gradient GEMMs on hipBLASLt (``dgrad_mm``). The projection weights' gradients are accumulated straight into the FP32
-masters' ``.grad`` with the FP32-accumulating GEMM, G += f32(r(dY^T X))
-(test_gradient_execution.py:243-246), in one grouped launch for the MLP's two weights;
-the function returns no gradient for them, so no BF16 weight gradient is materialised
-and autograd's own accumulation is bypassed for these parameters (one GPU: there is no
-gradient-bucket hook to feed). Every other parameter (norm weights, the tied head, the
-embedding and depth modulation) gets its gradient through autograd as usual.
+Each core piece is a registered operator (``warpstate::fused_norm_projection``,
+``warpstate::fused_residual_projection``, ``warpstate::fused_swiglu_block``) with a fake
+implementation and an autograd formula whose backward is another operator, so the patched
+core compiles with ``torch.compile(fullgraph=True)`` as the reference compiles its cores
+(run_40b.py:430-438). The backward operators are built from the fused backward kernels
+(the gate-sigmoid backward, the SwiGLU backward fused on the dAct GEMM, the RMSNorm
+backward) and ``dgrad_mm`` for the input gradients. A projection weight's gradient is
+f32(r(dY^T X)) from the FP32-accumulating GEMM (the MLP's two in one grouped launch),
+returned through autograd like the reference's BF16 dW (test_gradient_execution.py:243-246):
+autograd's accumulation into the FP32 master's ``.grad``, and any gradient hook (DDP's),
+see it as usual.
 
 A core call is eligible in training mode with gradients on, under BF16 autocast, on a BF16
 CUDA residual stream (``ops.residual_experiment.apply_bf16_residuals``) and bias-free
@@ -36,93 +38,178 @@ from ops import fused_execution as fx
 from ops._patching import bf16_autocast_training
 
 BF16 = torch.bfloat16
+F32 = torch.float32
+Tensor = torch.Tensor
+custom_op = torch.library.custom_op
 
 
-def _grad_buffer(param: torch.Tensor) -> torch.Tensor:
-    """The FP32 master's ``.grad``, created as zeros on first use."""
-    if param.grad is None:
-        param.grad = torch.zeros_like(param, memory_format=torch.contiguous_format)
-    grad = param.grad
-    if grad.dtype != torch.float32 or not grad.is_contiguous():
-        raise ValueError("Fused execution accumulates into contiguous FP32 .grad buffers")
-    return grad
+# --- norm1 -> in_proj -> gate sigmoid ------------------------------------------------------
+
+@custom_op("warpstate::fused_norm_projection", mutates_args=())
+def fused_norm_projection(x: Tensor, norm_weight: Tensor, weight: Tensor, eps: float,
+                          gate_begin: int, gate_end: int
+                          ) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """(P, rstd, y, W_bf16) for rows x [rows, d] BF16, the FP32 norm weight [d] and the
+    FP32 master W [n, d]: y = RMSNorm(x) in BF16, P = r(y @ W^T) with r(sigmoid) on columns
+    [gate_begin, gate_end). y and the BF16 weight are kept for the backward."""
+    w = weight.to(BF16)
+    normed = torch.empty_like(x)
+    out, rstd = fx.rmsnorm_gate_mm(x, norm_weight.contiguous(), eps, w, (gate_begin, gate_end),
+                                   normed=normed)
+    return out, rstd, normed, w
 
 
-class _NormProjection(torch.autograd.Function):
-    """P = r(RMSNorm(x) @ W^T) with r(sigmoid) on the gate columns, for x [rows, d] BF16,
-    the FP32 norm weight [d] and the FP32 master W [n, d]."""
-
-    @staticmethod
-    def forward(ctx, x, norm_weight, weight, eps, gate):
-        w = weight.to(BF16)
-        normed = torch.empty_like(x)
-        out, rstd = fx.rmsnorm_gate_mm(x, norm_weight.contiguous(), eps, w, gate, normed=normed)
-        ctx.save_for_backward(x, norm_weight, rstd, normed, w, out)
-        ctx.weight, ctx.gate = weight, gate
-        return out
-
-    @staticmethod
-    def backward(ctx, dout):
-        x, norm_weight, rstd, normed, w, out = ctx.saved_tensors
-        from ops.activation_execution import _rms_backward
-
-        dp = fx.sigmoid_backward_cols(dout.contiguous(), out, ctx.gate)
-        dy = fx.dgrad_mm(dp, w)
-        if ctx.needs_input_grad[2]:
-            fx.mm_accumulate_(_grad_buffer(ctx.weight), dp.T, normed, True)
-        dx, dnorm = _rms_backward(x, norm_weight, rstd, dy, True)
-        return dx, dnorm, None, None, None
+@fused_norm_projection.register_fake
+def _norm_projection_fake(x, norm_weight, weight, eps, gate_begin, gate_end):
+    return (x.new_empty((x.shape[0], weight.shape[0])), x.new_empty((x.shape[0],), dtype=F32),
+            torch.empty_like(x), weight.new_empty(weight.shape, dtype=BF16))
 
 
-class _ResidualProjection(torch.autograd.Function):
-    """r(R + r(A @ W^T)) for A [rows, k] BF16, the FP32 master W [n, k] and R [rows, n]."""
+@custom_op("warpstate::fused_norm_projection_backward", mutates_args=())
+def fused_norm_projection_backward(dout: Tensor, x: Tensor, norm_weight: Tensor, rstd: Tensor,
+                                   normed: Tensor, w: Tensor, out: Tensor, gate_begin: int,
+                                   gate_end: int) -> tuple[Tensor, Tensor, Tensor]:
+    """(dx, d norm_weight, dW): dP through the gate sigmoid, dy = r(dP @ W),
+    dW = f32(r(dP^T y)), then the RMSNorm backward with the saved rstd."""
+    from ops.activation_execution import _rms_backward
 
-    @staticmethod
-    def forward(ctx, a, weight, residual):
-        w = weight.to(BF16)
-        ctx.save_for_backward(a, w)
-        ctx.weight = weight
-        return fx.residual_mm(a, w, residual)
-
-    @staticmethod
-    def backward(ctx, dout):
-        a, w = ctx.saved_tensors
-        dout = dout.contiguous()
-        if ctx.needs_input_grad[1]:
-            fx.mm_accumulate_(_grad_buffer(ctx.weight), dout.T, a, True)
-        return fx.dgrad_mm(dout, w) if ctx.needs_input_grad[0] else None, None, dout
+    dp = fx.sigmoid_backward_cols(dout.contiguous(), out, (gate_begin, gate_end))
+    dy = fx.dgrad_mm(dp, w)
+    dw = torch.zeros(w.shape, dtype=F32, device=w.device)
+    fx.mm_accumulate_(dw, dp.T, normed, True)
+    dx, dnorm = _rms_backward(x, norm_weight, rstd, dy, True)
+    return dx, dnorm, dw
 
 
-class _SwiGLUBlock(torch.autograd.Function):
-    """R + down(silu(gate) * up) with (up | gate) = h @ W_upgate^T, in two launches (the
-    paired projection with the SwiGLU epilogue, then the down projection with the residual
-    epilogue), eager BF16 rounding throughout."""
+@fused_norm_projection_backward.register_fake
+def _norm_projection_backward_fake(dout, x, norm_weight, rstd, normed, w, out, gate_begin,
+                                   gate_end):
+    return (torch.empty_like(x), norm_weight.new_empty(norm_weight.shape, dtype=F32),
+            w.new_empty(w.shape, dtype=F32))
 
-    @staticmethod
-    def forward(ctx, h, w_upgate, w_down, residual):
-        from ops.matmul_epilogue import launch_swiglu_mm
 
-        wug, wd = w_upgate.to(BF16), w_down.to(BF16)
-        packed, act = launch_swiglu_mm(h, wug.T, "tiled", (128, 128, 32, 8, 3), True)
-        ctx.save_for_backward(h, wug, wd, packed, act)
-        ctx.weights = (w_upgate, w_down)
-        return fx.residual_mm(act, wd, residual)
+def _norm_projection_setup(ctx, inputs, output):
+    x, norm_weight, _weight, _eps, gate_begin, gate_end = inputs
+    out, rstd, normed, w = output
+    ctx.save_for_backward(x, norm_weight, rstd, normed, w, out)
+    ctx.gate = (gate_begin, gate_end)
 
-    @staticmethod
-    def backward(ctx, dout):
-        h, wug, wd, packed, act = ctx.saved_tensors
-        w_upgate, w_down = ctx.weights
-        dout = dout.contiguous()
-        dpacked = fx.swiglu_backward_mm(dout, wd, packed, True)
-        groups = []
-        if ctx.needs_input_grad[2]:
-            groups.append((_grad_buffer(w_down), dout.T, act))
-        if ctx.needs_input_grad[1]:
-            groups.append((_grad_buffer(w_upgate), dpacked.T, h))
-        fx.mm_accumulate_group_(groups, True)
-        dh = fx.dgrad_mm(dpacked, wug) if ctx.needs_input_grad[0] else None
-        return dh, None, None, dout
 
+def _norm_projection_autograd(ctx, dout, _drstd, _dnormed, _dw):
+    x, norm_weight, rstd, normed, w, out = ctx.saved_tensors
+    dx, dnorm, dweight = fused_norm_projection_backward(dout, x, norm_weight, rstd, normed, w,
+                                                        out, *ctx.gate)
+    return dx, dnorm, dweight, None, None, None
+
+
+fused_norm_projection.register_autograd(_norm_projection_autograd,
+                                        setup_context=_norm_projection_setup)
+
+
+# --- projection + residual -----------------------------------------------------------------
+
+@custom_op("warpstate::fused_residual_projection", mutates_args=())
+def fused_residual_projection(a: Tensor, weight: Tensor, residual: Tensor
+                              ) -> tuple[Tensor, Tensor]:
+    """(r(R + r(A @ W^T)), W_bf16) for A [rows, k] BF16, the FP32 master W [n, k] and the
+    BF16 residual R [rows, n]."""
+    w = weight.to(BF16)
+    return fx.residual_mm(a, w, residual), w
+
+
+@fused_residual_projection.register_fake
+def _residual_projection_fake(a, weight, residual):
+    return torch.empty_like(residual), weight.new_empty(weight.shape, dtype=BF16)
+
+
+@custom_op("warpstate::fused_residual_projection_backward", mutates_args=())
+def fused_residual_projection_backward(dout: Tensor, a: Tensor, w: Tensor
+                                       ) -> tuple[Tensor, Tensor]:
+    """(dA, dW): dA = r(dOut @ W), dW = f32(r(dOut^T A))."""
+    dout = dout.contiguous()
+    dw = torch.zeros(w.shape, dtype=F32, device=w.device)
+    fx.mm_accumulate_(dw, dout.T, a, True)
+    return fx.dgrad_mm(dout, w), dw
+
+
+@fused_residual_projection_backward.register_fake
+def _residual_projection_backward_fake(dout, a, w):
+    return torch.empty_like(a), w.new_empty(w.shape, dtype=F32)
+
+
+def _residual_projection_setup(ctx, inputs, output):
+    a, _weight, _residual = inputs
+    ctx.save_for_backward(a, output[1])
+
+
+def _residual_projection_autograd(ctx, dout, _dw):
+    a, w = ctx.saved_tensors
+    da, dweight = fused_residual_projection_backward(dout, a, w)
+    return da, dweight, dout
+
+
+fused_residual_projection.register_autograd(_residual_projection_autograd,
+                                            setup_context=_residual_projection_setup)
+
+
+# --- SwiGLU block + residual ---------------------------------------------------------------
+
+@custom_op("warpstate::fused_swiglu_block", mutates_args=())
+def fused_swiglu_block(h: Tensor, w_upgate: Tensor, w_down: Tensor, residual: Tensor
+                       ) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """(R + down(silu(gate) * up), packed, act, W_upgate_bf16, W_down_bf16) with
+    (up | gate) = h @ W_upgate^T: the paired projection with the SwiGLU epilogue, then the
+    down projection with the residual epilogue, eager BF16 rounding throughout."""
+    from ops.matmul_epilogue import launch_swiglu_mm
+
+    wug, wd = w_upgate.to(BF16), w_down.to(BF16)
+    packed, act = launch_swiglu_mm(h, wug.T, "tiled", (128, 128, 32, 8, 3), True)
+    return fx.residual_mm(act, wd, residual), packed, act, wug, wd
+
+
+@fused_swiglu_block.register_fake
+def _swiglu_block_fake(h, w_upgate, w_down, residual):
+    rows, two_h = h.shape[0], w_upgate.shape[0]
+    return (torch.empty_like(residual), h.new_empty((rows, two_h)),
+            h.new_empty((rows, two_h // 2)), w_upgate.new_empty(w_upgate.shape, dtype=BF16),
+            w_down.new_empty(w_down.shape, dtype=BF16))
+
+
+@custom_op("warpstate::fused_swiglu_block_backward", mutates_args=())
+def fused_swiglu_block_backward(dout: Tensor, h: Tensor, packed: Tensor, act: Tensor,
+                                wug: Tensor, wd: Tensor) -> tuple[Tensor, Tensor, Tensor]:
+    """(dh, dW_upgate, dW_down): dPacked from the dAct GEMM with the SwiGLU backward in its
+    epilogue, both weight gradients in one grouped FP32-accumulating launch, and
+    dh = r(dPacked @ W_upgate)."""
+    dout = dout.contiguous()
+    dpacked = fx.swiglu_backward_mm(dout, wd, packed, True)
+    g_upgate = torch.zeros(wug.shape, dtype=F32, device=wug.device)
+    g_down = torch.zeros(wd.shape, dtype=F32, device=wd.device)
+    fx.mm_accumulate_group_([(g_down, dout.T, act), (g_upgate, dpacked.T, h)], True)
+    return fx.dgrad_mm(dpacked, wug), g_upgate, g_down
+
+
+@fused_swiglu_block_backward.register_fake
+def _swiglu_block_backward_fake(dout, h, packed, act, wug, wd):
+    return (torch.empty_like(h), wug.new_empty(wug.shape, dtype=F32),
+            wd.new_empty(wd.shape, dtype=F32))
+
+
+def _swiglu_block_setup(ctx, inputs, output):
+    _out, packed, act, wug, wd = output
+    ctx.save_for_backward(inputs[0], packed, act, wug, wd)
+
+
+def _swiglu_block_autograd(ctx, dout, _dpacked, _dact, _dwug, _dwd):
+    h, packed, act, wug, wd = ctx.saved_tensors
+    dh, g_upgate, g_down = fused_swiglu_block_backward(dout, h, packed, act, wug, wd)
+    return dh, g_upgate, g_down, dout
+
+
+fused_swiglu_block.register_autograd(_swiglu_block_autograd, setup_context=_swiglu_block_setup)
+
+
+# --- the adapter ---------------------------------------------------------------------------
 
 def _core_eligible(core, x: torch.Tensor) -> bool:
     return (bf16_autocast_training(core, x) and x.dtype == BF16 and x.numel() > 0
@@ -137,13 +224,13 @@ def _fused_core_forward(core, x: torch.Tensor) -> torch.Tensor:
 
     d = core.in_proj.in_features
     rows = x.reshape(-1, d).contiguous()
-    p = _NormProjection.apply(rows, core.norm1.weight, core.in_proj.weight,
-                              float(core.norm1.eps), (3 * d, 4 * d))
+    p = fused_norm_projection(rows, core.norm1.weight, core.in_proj.weight,
+                              float(core.norm1.eps), 3 * d, 4 * d)[0]
     q, k, v, gate, u = p.view(*x.shape[:-1], 5 * d).chunk(5, dim=-1)
     mixed = core.mix(q, k, v, gate, u).reshape(-1, d).to(BF16).contiguous()
-    rows = _ResidualProjection.apply(mixed, core.out_proj.weight, rows)
+    rows = fused_residual_projection(mixed, core.out_proj.weight, rows)[0]
     h, _rstd = bf16_rmsnorm(rows, core.norm2.weight, float(core.norm2.eps), True)
-    rows = _SwiGLUBlock.apply(h, core.ffn.up_gate.weight, core.ffn.down.weight, rows)
+    rows = fused_swiglu_block(h, core.ffn.up_gate.weight, core.ffn.down.weight, rows)[0]
     return rows.view(x.shape)
 
 
