@@ -110,11 +110,6 @@ int64_t ws_rmsnorm_backward_static_max_partial_floats(void);
 int ws_transpose_bf16(const void* in, int64_t ld_in, void* out, int64_t rows, int64_t cols,
                       void* stream);
 
-/* Row statistics of RMSNorm: rstd[r] = 1/sqrt(mean_k f32(x[r,k])^2 + eps) for x with row
- * stride ldx (warpstate/model.py:26-27). */
-int ws_rms_rstd(const void* x, int64_t ldx, float* rstd, int64_t rows, int64_t d, float eps,
-                void* stream);
-
 /*
  * RMSNorm-prologue projection with gate sigmoid: out[m,n] = bf16(y @ B) with
  * y = r(r(x * rstd) * r(norm_weight)), then out[:, gate_begin:gate_end] = r(sigmoid(out)).

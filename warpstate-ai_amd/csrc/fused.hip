@@ -50,22 +50,6 @@ int launch_rmsnorm_rows(const void* x, long ldx, const float* w, void* y, float*
 }
 }  // namespace ws
 
-static int launch_rstd(const void* x, long ldx, float* rstd, long rows, long d, float eps,
-                       hipStream_t s) {
-  const int vec = (ldx % 8 == 0) && (d % 8 == 0) && al(x, 16);
-  hipLaunchKernelGGL(rms_rstd_kernel, dim3(cdiv(rows, 4)), dim3(256), 0, s,
-                     static_cast<const unsigned short*>(x), ldx, rstd, (int)rows, (int)d, eps, vec);
-  return hip_check(hipGetLastError(), "rms_rstd launch");
-}
-
-extern "C" int ws_rms_rstd(const void* x, int64_t ldx, float* rstd, int64_t rows, int64_t d,
-                           float eps, void* stream) {
-  if (!x || !rstd) return set_error(kInvalid, "null pointer");
-  if (rows < 1 || d < 1 || !fits_i32(rows) || !fits_i32(d) || ldx < d)
-    return set_error(kInvalid, "invalid RMSNorm shape");
-  return launch_rstd(x, ldx, rstd, rows, d, eps, static_cast<hipStream_t>(stream));
-}
-
 extern "C" int ws_rmsnorm_gate_mm(const void* x, int64_t x_s0, const float* norm_weight,
                                   float eps, float* rstd, void* normed, const void* b,
                                   int64_t b_s0, int64_t b_s1, void* out, int64_t m, int64_t n,

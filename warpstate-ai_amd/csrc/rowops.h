@@ -1,6 +1,6 @@
-// Row-wise and elementwise kernels of the hot path: RMSNorm statistics / forward /
-// backward, standalone SwiGLU forward / backward, cross-entropy reductions and
-// split-K reductions. All are HBM-bound; each reads and writes its operands once.
+// Row-wise and elementwise kernels of the hot path: RMSNorm forward / backward,
+// standalone SwiGLU forward / backward, cross-entropy reductions and split-K reductions.
+// All are HBM-bound; each reads and writes its operands once.
 #pragma once
 
 #include "common.h"
@@ -8,37 +8,6 @@
 namespace ws {
 
 // ---------------------------------------------------------------------------------------
-// RMSNorm row statistics: rstd[r] = 1 / sqrt(sum_k f32(x[r,k])^2 / D + eps)
-// (warpstate/model.py:26-27). One wave per row; the row sum is a wave-level butterfly
-// reduction (__shfl_xor lowers to DPP / ds_swizzle lane exchanges).
-static __global__ void __launch_bounds__(256) rms_rstd_kernel(const unsigned short* __restrict__ x,
-                                                       long ldx, float* __restrict__ rstd,
-                                                       int rows, int D, float eps, int vec) {
-  const int lane = threadIdx.x & 63;
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= rows) return;
-  const unsigned short* xr = x + (long)row * ldx;
-  float acc = 0.0f;
-  if (vec) {
-    for (int c = lane * 8; c < D; c += 64 * 8) {
-      u32x4_t v = *reinterpret_cast<const u32x4_t*>(xr + c);
-#pragma unroll
-      for (int d = 0; d < 4; ++d) {
-        float a = lo_bf16(v[d]), b = hi_bf16(v[d]);
-        acc += a * a;
-        acc += b * b;
-      }
-    }
-  } else {
-    for (int c = lane; c < D; c += 64) {
-      float a = bf16_bits_to_f32(xr[c]);
-      acc += a * a;
-    }
-  }
-  acc = wave_sum(acc);
-  if (lane == 0) rstd[row] = 1.0f / sqrtf(acc / (float)D + eps);
-}
-
 // RMSNorm of x (row stride ldx) into a contiguous BF16 y with the eager rounding of
 // RMSNorm.forward (warpstate/model.py:25-28): y = r(r(x * rstd) * r(w)); also stores
 // rstd. One wave per row; with `vec`, 16-byte loads and stores of 8 elements per lane.

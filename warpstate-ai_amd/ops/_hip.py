@@ -40,7 +40,6 @@ SIGNATURES = {
                                           _c_void_p, _c_void_p, _i64, _i64, _i32, _c_void_p]),
     "ws_rmsnorm_backward_static_max_partial_floats": (_i64, []),
     "ws_transpose_bf16": (_i32, [_c_void_p, _i64, _c_void_p, _i64, _i64, _c_void_p]),
-    "ws_rms_rstd": (_i32, [_c_void_p, _i64, _c_void_p, _i64, _i64, _f32, _c_void_p]),
     "ws_rmsnorm_gate_mm": (_i32, [_c_void_p, _i64, _c_void_p, _f32, _c_void_p, _c_void_p,
                                   _c_void_p, _i64, _i64, _c_void_p, _i64, _i64, _i64, _i64,
                                   _i64, _c_void_p]),
