@@ -403,8 +403,12 @@ def test_linear_cross_entropy_stored_logits_match_recompute_bitwise(rows, d, voc
 
 
 @pytest.mark.parametrize("m,d,vocab,chunk", [(512, 256, 1024, 2048), (300, 512, 4096, 128),
-                                             (1024, 2048, 8192, 512)])
+                                             (1024, 2048, 8192, 512), (1001, 256, 1030, 256),
+                                             (998, 128, 2048, 300)])
 def test_linear_cross_entropy(m, d, vocab, chunk):
+    """Against the oracle; the last two cases have row counts that are not a multiple of 4
+    (the mean's and count's last piece) and 10 or 16 statistics partials per row (one part
+    per lane, or 16-byte pieces)."""
     from ops.benchmark_configs import lm_head_inputs
     from ops.fused_execution import CrossEntropyState, linear_cross_entropy_backward, \
         linear_cross_entropy_forward
@@ -539,7 +543,7 @@ def test_rmsnorm_gate_projection_backward(m, d, n, gate, in_place):
 
 
 @pytest.mark.parametrize("rows,d,vocab,chunk", [(512, 256, 1024, 256), (3000, 384, 2052, 1024),
-                                                (700, 136, 1030, 512)])
+                                                (700, 136, 1030, 512), (1001, 128, 2048, 256)])
 def test_fused_cross_entropy_matches_the_two_pass_backward(rows, d, vocab, chunk):
     """The one-pass fused loss (chunk logits kept in the workspace, gradients formed while
     they are there) gives, for a unit upstream gradient, the two-pass loss, dHidden and

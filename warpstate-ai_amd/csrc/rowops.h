@@ -328,13 +328,38 @@ static __global__ void __launch_bounds__(256) ce_combine_kernel(const float* __r
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
-  float mx = -INFINITY;
-  for (int q = lane; q < parts; q += 64) mx = fmaxf(mx, part_max[(long)row * parts + q]);
-  mx = wave_max(mx);
-  float s = 0.0f;
-  for (int q = lane; q < parts; q += 64) {
-    float pm = part_max[(long)row * parts + q];
-    s += part_sum[(long)row * parts + q] * exp_e(pm - mx);
+  const float* pm = part_max + (long)row * parts;
+  const float* ps = part_sum + (long)row * parts;
+  float mx = -INFINITY, s = 0.0f;
+  // Rows of up to 1024 parts in 16-byte pieces: each lane requests all of its maxima and
+  // sums at once (4 consecutive parts per load), so a row costs one memory round trip and
+  // the sum runs on the registers. Other rows take one part per lane.
+  constexpr int kVec = 4;
+  const bool vec = (parts & 3) == 0 && parts <= 256 * kVec &&
+                   ((reinterpret_cast<unsigned long>(part_max) |
+                     reinterpret_cast<unsigned long>(part_sum)) & 15) == 0;
+  if (vec) {
+    f32x4_t m4[kVec], s4[kVec];
+#pragma unroll
+    for (int i = 0; i < kVec; ++i) {
+      const int q = 4 * lane + 256 * i;
+      const bool ok = q < parts;
+      m4[i] = ok ? *reinterpret_cast<const f32x4_t*>(pm + q) : f32x4_t{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+      s4[i] = ok ? *reinterpret_cast<const f32x4_t*>(ps + q) : f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+#pragma unroll
+    for (int i = 0; i < kVec; ++i)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) mx = fmaxf(mx, m4[i][e]);
+    mx = wave_max(mx);
+#pragma unroll
+    for (int i = 0; i < kVec; ++i)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) s += s4[i][e] * exp_e(m4[i][e] - mx);
+  } else {
+    for (int q = lane; q < parts; q += 64) mx = fmaxf(mx, pm[q]);
+    mx = wave_max(mx);
+    for (int q = lane; q < parts; q += 64) s += ps[q] * exp_e(pm[q] - mx);
   }
   s = wave_sum(s);
   if (lane == 0) {
@@ -358,9 +383,38 @@ static __global__ void __launch_bounds__(1024) ce_mean_kernel(const float* __res
   __shared__ long scnt[1024];
   float s = 0.0f;
   long c = 0;
-  for (int i = threadIdx.x; i < rows; i += 1024) {
-    s += loss[i];
-    c += targets[i] != -100 ? 1 : 0;
+  // Thread t takes rows 4t + 4096 u + 16384 j (u < 4): 16-byte loads of 4 losses and 2 x 2
+  // targets, all four pieces of a round requested before any is added, so 16384 rows cost
+  // one memory round trip. Rows past the end of a piece are read one by one.
+  const bool vec = ((reinterpret_cast<unsigned long>(loss) |
+                     reinterpret_cast<unsigned long>(targets)) & 15) == 0;
+  for (int base = 4 * (int)threadIdx.x; base < rows; base += 4 * 4096) {
+    f32x4_t lv[4];
+    long tv[4][4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int i = base + 4096 * u;
+      if (vec && i + 3 < rows) {
+        lv[u] = *reinterpret_cast<const f32x4_t*>(loss + i);
+        const i64x2_t t0 = *reinterpret_cast<const i64x2_t*>(targets + i);
+        const i64x2_t t1 = *reinterpret_cast<const i64x2_t*>(targets + i + 2);
+        tv[u][0] = t0[0]; tv[u][1] = t0[1]; tv[u][2] = t1[0]; tv[u][3] = t1[1];
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const bool ok = i + e < rows;
+          lv[u][e] = ok ? loss[i + e] : 0.0f;
+          tv[u][e] = ok ? targets[i + e] : -100;
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        s += lv[u][e];
+        c += tv[u][e] != -100 ? 1 : 0;
+      }
   }
   ssum[threadIdx.x] = s;
   scnt[threadIdx.x] = c;
@@ -380,13 +434,33 @@ static __global__ void __launch_bounds__(1024) ce_mean_kernel(const float* __res
 }
 
 // The valid-token count of the whole batch and the unit-upstream-gradient scale
-// 1 / max(1, count), before any chunk of the fused pass forms its gradients. One block.
+// 1 / max(1, count), before any chunk of the fused pass forms its gradients. One block;
+// the targets are read as in ce_mean_kernel.
 static __global__ void __launch_bounds__(1024) ce_count_kernel(const long* __restrict__ targets,
                                                         int rows, long* __restrict__ count_out,
                                                         float* __restrict__ scale) {
   __shared__ long scnt[1024];
   long c = 0;
-  for (int i = threadIdx.x; i < rows; i += 1024) c += targets[i] != -100 ? 1 : 0;
+  const bool vec = (reinterpret_cast<unsigned long>(targets) & 15) == 0;
+  for (int base = 4 * (int)threadIdx.x; base < rows; base += 4 * 4096) {
+    long tv[4][4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int i = base + 4096 * u;
+      if (vec && i + 3 < rows) {
+        const i64x2_t t0 = *reinterpret_cast<const i64x2_t*>(targets + i);
+        const i64x2_t t1 = *reinterpret_cast<const i64x2_t*>(targets + i + 2);
+        tv[u][0] = t0[0]; tv[u][1] = t0[1]; tv[u][2] = t1[0]; tv[u][3] = t1[1];
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) tv[u][e] = i + e < rows ? targets[i + e] : -100;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) c += tv[u][e] != -100 ? 1 : 0;
+  }
   scnt[threadIdx.x] = c;
   __syncthreads();
   for (int stride = 512; stride > 0; stride >>= 1) {
