@@ -127,7 +127,8 @@ inline int check_out_stride(long ld, int elem_bytes, const char* what) {
 template <int AM, int BMD, bool PAIRED, class Epi>
 int run_fast(GemmParams p, LaunchCfg cfg, hipStream_t stream) {
   const void* kern = reinterpret_cast<const void*>(&gemm_fast_kernel<AM, BMD, PAIRED, Epi>);
-  if (int rc = ensure_lds(kern, kFLdsAlloc)) return rc;
+  constexpr int lds_bytes = fast_lds_bytes<AM, BMD>();
+  if (int rc = ensure_lds(kern, lds_bytes)) return rc;
   const int cols = PAIRED ? p.H : p.N;
   const int bn_cols = PAIRED ? kFBN / 2 : kFBN;
   p.tiles_m = cdiv(p.M, kFBM);
@@ -141,7 +142,7 @@ int run_fast(GemmParams p, LaunchCfg cfg, hipStream_t stream) {
   dim3 grid(cfg.persistent ? (p.total_tiles < resident ? p.total_tiles : resident) : p.total_tiles,
             splits);
   if (cfg.workers > 0) grid = dim3(cfg.workers, 1);
-  hipLaunchKernelGGL((gemm_fast_kernel<AM, BMD, PAIRED, Epi>), grid, dim3(kFNT), kFLdsAlloc, stream, p);
+  hipLaunchKernelGGL((gemm_fast_kernel<AM, BMD, PAIRED, Epi>), grid, dim3(kFNT), lds_bytes, stream, p);
   return hip_check(hipGetLastError(), "gemm launch");
 }
 
