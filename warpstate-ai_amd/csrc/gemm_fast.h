@@ -34,9 +34,14 @@
 //    steps the loads of B two tiles ahead. Those land while the second step runs without
 //    LDS reads, and only half a tile's loads leave in a burst after the barrier (the
 //    forward GEMMs 3-7 % faster than with both operands' next tile loaded there).
-//  * With an M/N-contiguous operand both operands have two stages and the next tile's
-//    loads are issued between the two steps (after the tile's last fragment read), which
-//    keeps their LDS writes away from the transposing reads.
+//  * Both operands M/N-contiguous (the weight gradients): two stages of 64 KiB; after the
+//    barrier the next tile's loads for both operands, then the transposing fragment reads.
+//    The reads are inline assembly with explicit lgkmcnt waits: the compiler orders the
+//    transposing-read builtin after every pending direct-to-LDS load (it cannot rule out
+//    an alias), which would otherwise hold those loads back until after the tile's last
+//    read and leave them half a k-tile of lead (the weight gradients 9 % slower).
+//  * One operand of each kind: both in two stages, the next tile's loads between the two
+//    steps (after the tile's last transposing read).
 //  * Tiles follow the grouped raster of ops/matmul_kernels.py:72-78 after an XCD remap.
 #pragma once
 
@@ -176,6 +181,42 @@ __device__ __forceinline__ bf16x8_t read_frag(const unsigned char* tile, int rb,
     i16x8_t v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
     return __builtin_bit_cast(bf16x8_t, v);
   }
+}
+
+// Transposing fragment reads as inline assembly, for the loop with both operands
+// M/N-contiguous. The compiler does not see them as LDS accesses, so the direct-to-LDS
+// loads of the next tile may be issued before them without an added vmcnt wait; their
+// results are made visible by tie_wait, an explicit lgkmcnt(0) that redefines the
+// fragment registers, so no MFMA reading them can be scheduled ahead of the wait.
+template <int OFF>
+__device__ __forceinline__ u32x2_t tr_read(unsigned addr) {
+  u32x2_t v;
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF) : "memory");
+  return v;
+}
+// Fragment of k32 step S at LDS byte address `addr` (tr_base plus the stage offset): the
+// two reads of read_frag<kMNContig>, k-rows kk0 and kk0 + 4 (the same swizzle, 512 bytes
+// apart); step 1 is 32 k-rows (4096 bytes) further with the same swizzle.
+template <int S>
+__device__ __forceinline__ bf16x8_t tr_frag(unsigned addr) {
+  const u32x2_t lo = tr_read<S * 4096>(addr), hi = tr_read<S * 4096 + 512>(addr);
+  const u32x4_t v = {lo[0], lo[1], hi[0], hi[1]};
+  return __builtin_bit_cast(bf16x8_t, v);
+}
+// Byte offset, within an M/N-contiguous operand tile, of lane's first read of the
+// fragment of the 16-row block at tile row rb, k32 step 0 (read_frag<kMNContig>).
+__device__ __forceinline__ unsigned tr_base(int rb, int lane) {
+  const int L = lane & 15, g = lane >> 4;
+  const int m = rb + 4 * (L & 3);
+  const int kk0 = 8 * g + (L >> 2);
+  const int blk = (m >> 6) * 8192, c = (m >> 3) & 7, hb = (m & 4) * 2;
+  return (unsigned)(blk + kk0 * 128 + ((c ^ mnsw(kk0)) << 4) + hb);
+}
+__device__ __forceinline__ void tie_wait(bf16x8_t (&f)[12]) {
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(f[0]), "+v"(f[1]), "+v"(f[2]), "+v"(f[3]), "+v"(f[4]), "+v"(f[5]),
+                 "+v"(f[6]), "+v"(f[7]), "+v"(f[8]), "+v"(f[9]), "+v"(f[10]), "+v"(f[11])
+               :: "memory");
 }
 
 template <int FA, int FB>
@@ -633,6 +674,8 @@ __global__ void __launch_bounds__(kFNT) gemm_fast_kernel(const GemmParams p) {
   // faster). With both operands K-contiguous, A keeps the full k-tile of lead time
   // (issuing it mid-tile costs 10 % there) and B, with a third stage, two k-tiles.
   constexpr bool kMidIssue = AMODE == kMNContig || BMODE == kMNContig;
+  // Both operands M/N-contiguous (and not paired): the loop with assembly fragment reads.
+  constexpr bool kBothMN = AMODE == kMNContig && BMODE == kMNContig && !PAIRED;
 
   extern __shared__ __attribute__((aligned(1024))) unsigned char fsmem[];
   if (p.skip_if != nullptr && *p.skip_if != 0) return;  // uniform: the whole grid exits
@@ -733,6 +776,58 @@ __global__ void __launch_bounds__(kFNT) gemm_fast_kernel(const GemmParams p) {
       // The zero-filling loads of the last two k-tiles land, and every wave is done reading,
       // before the epilogue's staging writes and the next tile's first loads.
       __builtin_amdgcn_s_waitcnt(wait_vmcnt(0));
+      __builtin_amdgcn_s_barrier();
+    } else if (kb < ke && kBothMN) {
+      static_assert(FA + FB == 12, "tie_wait binds 12 fragments");
+      const unsigned lds0 =
+          (unsigned)(unsigned long)(__attribute__((address_space(3))) unsigned char*)fsmem;
+      unsigned abase[FA], bbase[FB];
+#pragma unroll
+      for (int i = 0; i < FA; ++i) abase[i] = lds0 + tr_base(wm * TM + 16 * i, lane);
+#pragma unroll
+      for (int j = 0; j < FB; ++j) bbase[j] = lds0 + kFTileBytes + tr_base(b_rb[j], lane);
+      la.issue(q.a, row0_a, kb * kFBK, p.K, fsmem, wave, lane);
+      lb.issue(q.b, row0_b, kb * kFBK, p.K, fsmem + kFTileBytes, wave, lane);
+      for (int kt = kb; kt < ke; ++kt) {
+        const int cur = (kt - kb) & 1;
+        __builtin_amdgcn_s_waitcnt(wait_vmcnt(0));
+        __builtin_amdgcn_s_barrier();
+        // The next tile's loads first: a full k-tile of lead.
+        if (kt + 1 < ke) {
+          unsigned char* nxt = fsmem + (cur ^ 1) * kFStageBytes;
+          la.issue(q.a, row0_a, (kt + 1) * kFBK, p.K, nxt, wave, lane);
+          lb.issue(q.b, row0_b, (kt + 1) * kFBK, p.K, nxt + kFTileBytes, wave, lane);
+        }
+        const unsigned st = (unsigned)(cur * kFStageBytes);
+        __builtin_amdgcn_sched_barrier(0);
+        bf16x8_t f0[FA + FB], f1[FA + FB];  // steps 0 and 1: A blocks, then B blocks
+#pragma unroll
+        for (int i = 0; i < FA; ++i) f0[i] = tr_frag<0>(abase[i] + st);
+#pragma unroll
+        for (int j = 0; j < FB; ++j) f0[FA + j] = tr_frag<0>(bbase[j] + st);
+        tie_wait(f0);
+        __builtin_amdgcn_sched_barrier(0);
+        // Step 0's MFMAs, step 1's fragment r read after MFMA ceil(r NM / 12).
+#pragma unroll
+        for (int n = 0; n < NM; ++n) {
+          const int i = n / FB, j = n % FB;
+          acc.v[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(f0[FA + j], f0[i], acc.v[i][j], 0, 0, 0);
+          if ((n * (FA + FB)) % NM < FA + FB) {
+            const int r = n * (FA + FB) / NM;
+            f1[r] = r < FA ? tr_frag<1>(abase[r] + st) : tr_frag<1>(bbase[r - FA] + st);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        tie_wait(f1);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < FA; ++i)
+#pragma unroll
+          for (int j = 0; j < FB; ++j)
+            acc.v[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(f1[FA + j], f1[i], acc.v[i][j], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      // All waves are done reading both stages before the next tile's first load.
       __builtin_amdgcn_s_barrier();
     } else if (kb < ke) {
       la.issue(q.a, row0_a, kb * kFBK, p.K, fsmem, wave, lane);
