@@ -537,22 +537,28 @@ struct FEpiCEStats {
                                              unsigned char* stage) {
     opaque_lane(lane);
     const int part = tn * kFWN + wn;
+    const int c0 = 4 * (lane >> 4);  // this lane's first column of each 16-column block
+    const int ncols = p.N - n_base;  // columns of this wave inside the vocabulary
 #pragma unroll
     for (int i = 0; i < FA; ++i) {
       const int m = m_base + 16 * i + (lane & 15);
       const bool mok = m < p.M;
-      const long tgt = mok ? p.targets[m] : -1;
-      float mx = -INFINITY;
+      // The row's target as a column of this wave's 128 (-1 if outside): one 32-bit compare
+      // and select per element, one store per row.
+      const long trel = (mok ? p.targets[m] : -1) - n_base;
+      const int t = trel >= 0 && trel < FB * 16 && trel < ncols ? (int)trel : -1;
+      float mx = -INFINITY, tv = 0.0f;
 #pragma unroll
       for (int j = 0; j < FB; ++j)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const int n = n_base + 16 * j + 4 * (lane >> 4) + e;
+          const int col = 16 * j + c0 + e;
           const float x = rbf16(acc.v[i][j][e]);
           acc.v[i][j][e] = x;
-          if (n < p.N) mx = fmaxf(mx, x);
-          if ((long)n == tgt && n < p.N) p.tgt_logit[m] = x;
+          if (col < ncols) mx = fmaxf(mx, x);
+          tv = col == t ? x : tv;
         }
+      if (t >= c0 && t < c0 + 16 * FB && ((t - c0) & 12) == 0) p.tgt_logit[m] = tv;
       mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
       mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
       float sum = 0.0f;
@@ -560,8 +566,8 @@ struct FEpiCEStats {
       for (int j = 0; j < FB; ++j)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const int n = n_base + 16 * j + 4 * (lane >> 4) + e;
-          if (n < p.N) sum += exp_e(acc.v[i][j][e] - mx);
+          const int col = 16 * j + c0 + e;
+          if (col < ncols) sum += exp_e(acc.v[i][j][e] - mx);
         }
       sum += __shfl_xor(sum, 16, kWave);
       sum += __shfl_xor(sum, 32, kWave);
