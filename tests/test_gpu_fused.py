@@ -26,9 +26,13 @@ def _gen(seed):
 
 @pytest.mark.parametrize("algorithm", ["tiled", "persistent"])
 @pytest.mark.parametrize("eager_rounding", [False, True])
-@pytest.mark.parametrize("shape", [(13, 46, 31), (128, 256, 128), (257, 192, 193), (512, 1024, 256)])
+@pytest.mark.parametrize("shape", [(13, 46, 31), (128, 256, 128), (257, 192, 193), (512, 1024, 256),
+                                   (300, 272, 200), (520, 528, 1000)])
 @pytest.mark.parametrize("tile", [(64, 64, 32, 4, 3), (128, 128, 32, 8, 3)])
 def test_swiglu_projection_and_activation(algorithm, eager_rounding, shape, tile):
+    """(M, 2H, K). The last two shapes take the 256 x 256 paired kernel (K a multiple of 8)
+    with every edge ragged: partial row tiles, a half width H that is not a multiple of
+    the 128 columns a paired tile holds per half, and a partial last k-tile."""
     from ops.matmul_epilogue import launch_swiglu_mm
 
     m, packed_width, k = shape
