@@ -163,7 +163,7 @@ def run_step(inp, out, dp, timer=None):
         rmsnorm_gate_mm(inp["qkv_x"], inp["qkv_norm_weight"], inp["qkv_eps"], inp["qkv_w"],
                         GATE, out=out["qkv"], rstd=out["rstd"], normed=out["qkv_z"])
     with reg("swiglu_fwd"):
-        packed, act = launch_swiglu_mm(inp["mlp_x"], inp["mlp_w_upgate"].T, "tiled",
+        packed, act = launch_swiglu_mm(inp["mlp_x"], inp["mlp_w_upgate"].T, "persistent",
                                        (128, 128, 32, 8, 3), True)
     with reg("down_fwd"):
         residual_mm(inp["down_h"], inp["down_w_down"], inp["down_residual"], out=out["down"])
@@ -313,11 +313,11 @@ def bench_extra(args, device):
     c1 = swiglu_forward_inputs(seed=0)
     x, w = c1["x"].to(device), c1["w_upgate"].to(device)
     for _ in range(args.warmup):
-        launch_swiglu_mm(x, w.T, "tiled", (128, 128, 32, 8, 3), True)
+        launch_swiglu_mm(x, w.T, "persistent", (128, 128, 32, 8, 3), True)
     t = Timer()
     for _ in range(args.steps):
         with t.region("c1"):
-            launch_swiglu_mm(x, w.T, "tiled", (128, 128, 32, 8, 3), True)
+            launch_swiglu_mm(x, w.T, "persistent", (128, 128, 32, 8, 3), True)
     torch.cuda.synchronize()
     f1 = 2 * 4096 * 1024 * 5632
     ms = t.mean_ms("c1")

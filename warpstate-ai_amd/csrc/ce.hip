@@ -59,9 +59,9 @@ extern "C" int ws_linear_ce_forward(const void* hidden, int64_t ld_hidden, const
       return set_error(kInvalid, "stored logits need row-contiguous hidden and weight operands");
     p.c = static_cast<unsigned short*>(logits);
     p.ldc = vocab;
-    if (int rc = dispatch_fast<false, FEpiCEStatsLogits>(p, am, bm, LaunchCfg{0, 1}, s)) return rc;
+    if (int rc = dispatch_fast<false, FEpiCEStatsLogits>(p, am, bm, kFusedCfg, s)) return rc;
   } else if (fast_ok(p, am, bm, false)) {
-    if (int rc = dispatch_fast<false, FEpiCEStats>(p, am, bm, LaunchCfg{0, 1}, s)) return rc;
+    if (int rc = dispatch_fast<false, FEpiCEStats>(p, am, bm, kFusedCfg, s)) return rc;
   } else if (int rc = dispatch<kMaskKK | kMaskGG, WS_TILE_ARGS_LARGE, false, EpiCEStats>(
                  p, am, bm, LaunchCfg{0, 1}, s)) {
     return rc;
@@ -133,7 +133,7 @@ static int ce_chunk_gradients(const CeChunk& c, const void* weight, long ld_weig
   p.grad_scale = scale;
   p.skip_if = skip;
   int am = operand_mode(p.a, c.r, d, 256), bm = operand_mode(p.b, vocab, d, 256);
-  if (fast_ok(p, am, bm, false)) return dispatch_fast<false, FEpiCEGrad>(p, am, bm, LaunchCfg{0, 1}, s);
+  if (fast_ok(p, am, bm, false)) return dispatch_fast<false, FEpiCEGrad>(p, am, bm, kFusedCfg, s);
   return dispatch<kMaskKK | kMaskGG, WS_TILE_ARGS_LARGE, false, EpiCEGrad>(p, am, bm,
                                                                           LaunchCfg{0, 1}, s);
 }
@@ -186,7 +186,7 @@ static int ce_chunk_dhidden(const CeChunk& c, const unsigned short* gl, const vo
   }
   q.c = out;
   q.ldc = ld_out;
-  if (fast) return dispatch_fast<false, FEpiStore<false, false>>(q, qa, qb, LaunchCfg{0, 1}, s);
+  if (fast) return dispatch_fast<false, FEpiStore<false, false>>(q, qa, qb, kFusedCfg, s);
   return dispatch<kMaskMM, WS_TILE_ARGS_LARGE, false, EpiStore<false, false>>(q, qa, qb,
                                                                              LaunchCfg{0, 1}, s);
 }
@@ -313,9 +313,9 @@ extern "C" int ws_linear_ce_fused(const void* hidden, int64_t ld_hidden, const v
     if (store) {
       p.c = gl;
       p.ldc = vocab;
-      if (int rc = dispatch_fast<false, FEpiCEStatsLogits>(p, am, bm, LaunchCfg{0, 1}, s)) return rc;
+      if (int rc = dispatch_fast<false, FEpiCEStatsLogits>(p, am, bm, kFusedCfg, s)) return rc;
     } else if (fast_ok(p, am, bm, false)) {
-      if (int rc = dispatch_fast<false, FEpiCEStats>(p, am, bm, LaunchCfg{0, 1}, s)) return rc;
+      if (int rc = dispatch_fast<false, FEpiCEStats>(p, am, bm, kFusedCfg, s)) return rc;
     } else if (int rc = dispatch<kMaskKK | kMaskGG, WS_TILE_ARGS_LARGE, false, EpiCEStats>(
                    p, am, bm, LaunchCfg{0, 1}, s)) {
       return rc;

@@ -75,7 +75,7 @@ extern "C" int ws_rmsnorm_gate_mm(const void* x, int64_t x_s0, const float* norm
   p.gate_hi = (int)gate_end;
   int am = operand_mode(p.a, m, k, 256), bm = operand_mode(p.b, n, k, 256);
   if (fast_ok(p, am, bm, false))
-    return dispatch_fast<false, FEpiStore<true, false>>(p, am, bm, LaunchCfg{0, 1}, s);
+    return dispatch_fast<false, FEpiStore<true, false>>(p, am, bm, kFusedCfg, s);
   return dispatch<kMaskMM, WS_TILE_ARGS_LARGE, false, EpiStore<true, false>>(p, am, bm,
                                                                                    LaunchCfg{0, 1}, s);
 }
@@ -100,7 +100,7 @@ extern "C" int ws_residual_mm(const void* a, int64_t a_s0, int64_t a_s1, const v
   int am = operand_mode(p.a, m, k, 256), bm = operand_mode(p.b, n, k, 256);
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (fast_ok(p, am, bm, false))
-    return dispatch_fast<false, FEpiStore<false, true>>(p, am, bm, LaunchCfg{0, 1}, s);
+    return dispatch_fast<false, FEpiStore<false, true>>(p, am, bm, kFusedCfg, s);
   constexpr unsigned mask = kMaskKK | ab_bit(kKContig, kMNContig) | kMaskGG;
   return dispatch<mask, WS_TILE_ARGS_LARGE, false, EpiStore<false, true>>(
       p, am, bm, LaunchCfg{0, 1}, s);
@@ -127,7 +127,7 @@ extern "C" int ws_swiglu_backward_mm(const void* grad, int64_t g_s0, int64_t g_s
   int am = operand_mode(p.a, m, k, 256), bm = operand_mode(p.b, h, k, 256);
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (fast_ok(p, am, bm, false))
-    return dispatch_fast<false, FEpiSwigluBwd>(p, am, bm, LaunchCfg{0, 1}, s);
+    return dispatch_fast<false, FEpiSwigluBwd>(p, am, bm, kFusedCfg, s);
   constexpr unsigned mask = kMaskKK | ab_bit(kKContig, kMNContig) | kMaskGG;
   return dispatch<mask, WS_TILE_ARGS_LARGE, false, EpiSwigluBwd>(
       p, am, bm, LaunchCfg{0, 1}, s);
