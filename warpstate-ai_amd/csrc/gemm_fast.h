@@ -353,6 +353,7 @@ struct FEpiSwiglu {
     __amdgpu_buffer_rsrc_t rp = make_rsrc(p.c + (long)m_base * p.ldc + n_base, 0x7fffffff);
     __amdgpu_buffer_rsrc_t ra = make_rsrc(p.c2 + (long)m_base * p.ldc2 + n_base, 0x7fffffff);
     const long hoff = p.H;
+    const bool eager = p.eager;
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
       const int r = 8 * q + (lane >> 3);
@@ -360,11 +361,20 @@ struct FEpiSwiglu {
       const u32x4_t vu = *reinterpret_cast<const u32x4_t*>(stage + r * kFStageRow + c8 * 2);
       const u32x4_t vg = *reinterpret_cast<const u32x4_t*>(stage + r * kFStageRow + (64 + c8) * 2);
       u32x4_t va;
+      // The rounding mode is tested once per row group, not per element (the compiler
+      // otherwise computes both and selects).
+      if (eager) {
+        // The pair's two SiLU values rounded by one packed conversion.
 #pragma unroll
-      for (int d = 0; d < 4; ++d) {
-        float s0 = silu(lo_bf16(vg[d])), s1 = silu(hi_bf16(vg[d]));
-        if (p.eager) { s0 = rbf16(s0); s1 = rbf16(s1); }
-        va[d] = pack_bf16x2(s0 * lo_bf16(vu[d]), s1 * hi_bf16(vu[d]));
+        for (int d = 0; d < 4; ++d) {
+          unsigned ws = pack_bf16x2(silu(lo_bf16(vg[d])), silu(hi_bf16(vg[d])));
+          asm volatile("" : "+v"(ws));  // keeps the conversion packed
+          va[d] = pack_bf16x2(lo_bf16(ws) * lo_bf16(vu[d]), hi_bf16(ws) * hi_bf16(vu[d]));
+        }
+      } else {
+#pragma unroll
+        for (int d = 0; d < 4; ++d)
+          va[d] = pack_bf16x2(silu(lo_bf16(vg[d])) * lo_bf16(vu[d]), silu(hi_bf16(vg[d])) * hi_bf16(vu[d]));
       }
       const long po = (long)r * p.ldc + c8, ao = (long)r * p.ldc2 + c8;
       if (full) {
@@ -386,15 +396,29 @@ struct FEpiSwiglu {
 // projection is read, and dPacked written, as 16-byte row-contiguous pieces (8 columns
 // per lane, 16 lanes per 128-column row, 4 rows per instruction, 16 rows in flight).
 struct FEpiSwigluBwd {
-  __device__ __forceinline__ static void math(const GemmParams& p, float dy, float up, float gate,
-                                              float& du, float& dg) {
-    const float sg = sigmoid(gate);
-    float s = gate * sg;
-    if (p.eager) s = rbf16(s);
-    float dsilu = dy * up;
-    if (p.eager) dsilu = rbf16(dsilu);
-    du = dy * s;
-    dg = (dsilu * sg) * (1.0f + gate * (1.0f - sg));
+  // Two elements, the low and high BF16 halves of the dAct, up and gate words, to the
+  // packed dUp and dGate words. Under eager rounding the pair's s and dsilu each go
+  // through one packed conversion (the same round-to-nearest-even as one at a time).
+  template <bool EAGER>
+  __device__ __forceinline__ static void math2(unsigned wd, unsigned wu, unsigned wg,
+                                               unsigned& du, unsigned& dg) {
+    const float dy0 = lo_bf16(wd), dy1 = hi_bf16(wd);
+    const float g0 = lo_bf16(wg), g1 = hi_bf16(wg);
+    const float sg0 = sigmoid(g0), sg1 = sigmoid(g1);
+    float s0 = g0 * sg0, s1 = g1 * sg1;
+    float ds0 = dy0 * lo_bf16(wu), ds1 = dy1 * hi_bf16(wu);
+    if (EAGER) {
+      unsigned ws = pack_bf16x2(s0, s1), wds = pack_bf16x2(ds0, ds1);
+      // Opaque to the compiler, which would otherwise convert each half on its own.
+      asm volatile("" : "+v"(ws), "+v"(wds));
+      s0 = lo_bf16(ws);
+      s1 = hi_bf16(ws);
+      ds0 = lo_bf16(wds);
+      ds1 = hi_bf16(wds);
+    }
+    du = pack_bf16x2(dy0 * s0, dy1 * s1);
+    dg = pack_bf16x2((ds0 * sg0) * (1.0f + g0 * (1.0f - sg0)),
+                     (ds1 * sg1) * (1.0f + g1 * (1.0f - sg1)));
   }
   template <int FA, int FB>
   __device__ __forceinline__ static void run(const GemmParams& p, Acc16<FA, FB>& acc, int m_base,
@@ -437,28 +461,33 @@ struct FEpiSwigluBwd {
           vu[q][h] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rp, store_off(ok, off, 2), 0, kEpiNT));
           vg[q][h] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rp, store_off(ok, off + hoff, 2), 0, kEpiNT));
         }
+      // The rounding mode is tested once here, not per element (the compiler otherwise
+      // computes both and selects).
+      auto finish = [&](auto eager) {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
+        for (int q = 0; q < 4; ++q) {
 #pragma unroll
-        for (int h = 0; h < 4; ++h) {
-          const int r = 16 * q + 4 * h + (lane >> 4);
-          const int m = m_base + r;
-          const bool ok = m < p.M && n + 7 < p.N;
-          const u32x4_t vd = *reinterpret_cast<const u32x4_t*>(stage + r * kFStageRow + c8 * 2);
-          u32x4_t od, og;
+          for (int h = 0; h < 4; ++h) {
+            const int r = 16 * q + 4 * h + (lane >> 4);
+            const int m = m_base + r;
+            const bool ok = m < p.M && n + 7 < p.N;
+            const u32x4_t vd = *reinterpret_cast<const u32x4_t*>(stage + r * kFStageRow + c8 * 2);
+            u32x4_t od, og;
 #pragma unroll
-          for (int d = 0; d < 4; ++d) {
-            float du0, dg0, du1, dg1;
-            math(p, lo_bf16(vd[d]), lo_bf16(vu[q][h][d]), lo_bf16(vg[q][h][d]), du0, dg0);
-            math(p, hi_bf16(vd[d]), hi_bf16(vu[q][h][d]), hi_bf16(vg[q][h][d]), du1, dg1);
-            od[d] = pack_bf16x2(du0, du1);
-            og[d] = pack_bf16x2(dg0, dg1);
+            for (int d = 0; d < 4; ++d) {
+              unsigned wu, wg;
+              math2<decltype(eager)::value>(vd[d], vu[q][h][d], vg[q][h][d], wu, wg);
+              od[d] = wu;
+              og[d] = wg;
+            }
+            const long off = (long)r * p.ldc + c8;
+            __builtin_amdgcn_raw_buffer_store_b128(od, rd, store_off(ok, off, 2), 0, kEpiNT);
+            __builtin_amdgcn_raw_buffer_store_b128(og, rd, store_off(ok, off + hoff, 2), 0, kEpiNT);
           }
-          const long off = (long)r * p.ldc + c8;
-          __builtin_amdgcn_raw_buffer_store_b128(od, rd, store_off(ok, off, 2), 0, kEpiNT);
-          __builtin_amdgcn_raw_buffer_store_b128(og, rd, store_off(ok, off + hoff, 2), 0, kEpiNT);
         }
-      }
+      };
+      if (p.eager) finish(std::true_type{});
+      else finish(std::false_type{});
     }
   }
 };
