@@ -568,36 +568,58 @@ struct FEpiCEStats {
     const int part = tn * kFWN + wn;
     const int c0 = 4 * (lane >> 4);  // this lane's first column of each 16-column block
     const int ncols = p.N - n_base;  // columns of this wave inside the vocabulary
+    // Columns past the vocabulary (only in a ragged last column tile: a wave-uniform test)
+    // become -inf, so the max and the sum below need no per-element column test: such a
+    // column adds exp(-inf) = 0. A wave with no column inside takes 0 as the sum's
+    // reference point instead of its max of -inf, and writes max -inf and sum 0.
+    if (ncols < FB * 16) {
+#pragma unroll
+      for (int i = 0; i < FA; ++i)
+#pragma unroll
+        for (int j = 0; j < FB; ++j)
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (16 * j + c0 + e >= ncols) acc.v[i][j][e] = -INFINITY;
+    }
 #pragma unroll
     for (int i = 0; i < FA; ++i) {
       const int m = m_base + 16 * i + (lane & 15);
       const bool mok = m < p.M;
-      // The row's target as a column of this wave's 128 (-1 if outside): one 32-bit compare
-      // and select per element, one store per row.
+      // The row's target as a column of this wave's 128 (-1 if outside).
       const long trel = (mok ? p.targets[m] : -1) - n_base;
       const int t = trel >= 0 && trel < FB * 16 && trel < ncols ? (int)trel : -1;
-      float mx = -INFINITY, tv = 0.0f;
+      float mx = -INFINITY;
 #pragma unroll
       for (int j = 0; j < FB; ++j)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int col = 16 * j + c0 + e;
-          const float x = rbf16(acc.v[i][j][e]);
-          acc.v[i][j][e] = x;
-          if (col < ncols) mx = fmaxf(mx, x);
-          tv = col == t ? x : tv;
+        for (int e = 0; e < 4; e += 2) {
+          // Two neighbouring logits rounded by one packed conversion (opaque to the
+          // compiler, which would otherwise convert each on its own).
+          unsigned w = pack_bf16x2(acc.v[i][j][e], acc.v[i][j][e + 1]);
+          asm volatile("" : "+v"(w));
+          acc.v[i][j][e] = lo_bf16(w);
+          acc.v[i][j][e + 1] = hi_bf16(w);
+          mx = fmaxf(fmaxf(mx, acc.v[i][j][e]), acc.v[i][j][e + 1]);
         }
-      if (t >= c0 && t < c0 + 16 * FB && ((t - c0) & 12) == 0) p.tgt_logit[m] = tv;
+      // The target logit: a 32-bit compare and select per element, only in the waves where
+      // some row's target falls in these columns (1 in 16 for a 32768 vocabulary), and one
+      // store per row.
+      if (__builtin_amdgcn_ballot_w64(t >= 0) != 0) {
+        float tv = 0.0f;
+#pragma unroll
+        for (int j = 0; j < FB; ++j)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) tv = 16 * j + c0 + e == t ? acc.v[i][j][e] : tv;
+        if (t >= c0 && t < c0 + 16 * FB && ((t - c0) & 12) == 0) p.tgt_logit[m] = tv;
+      }
       mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
       mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+      const float ref = ncols > 0 ? mx : 0.0f;
       float sum = 0.0f;
 #pragma unroll
       for (int j = 0; j < FB; ++j)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int col = 16 * j + c0 + e;
-          if (col < ncols) sum += exp_e(acc.v[i][j][e] - mx);
-        }
+        for (int e = 0; e < 4; ++e) sum += exp_e(acc.v[i][j][e] - ref);
       sum += __shfl_xor(sum, 16, kWave);
       sum += __shfl_xor(sum, 32, kWave);
       if (mok && lane < 16) {
