@@ -171,22 +171,29 @@ static int ce_chunk_dhidden(const CeChunk& c, const unsigned short* gl, const vo
   q.M = (int)c.r; q.N = (int)d; q.K = (int)vocab;
   q.skip_if = skip;
   int qa = operand_mode(q.a, c.r, vocab, 256), qb = operand_mode(q.b, d, vocab, 256);
-  q.vec_out = (d % 4 == 0) && (ld_out % 4 == 0) && (reinterpret_cast<unsigned long>(out) % 8 == 0);
-  const bool fast = fast_ok(q, qa, qb, false);
-  if (splits > 1 && fast) {
+  if (splits > 1) {
+    // FP32 slices of the vocabulary through the workspace, on the fast kernel when the
+    // operands allow it and on the generic one otherwise (a vocabulary that is not a
+    // multiple of 8 leaves the logit-gradient rows without 16-byte alignment): with few
+    // row tiles an unsplit launch would run the whole vocabulary on a handful of CUs.
     q.g = partials;
     q.ldg = d;
     q.split_stride = chunk * d;
     q.vec_out = (d % 4 == 0);
-    if (int rc = dispatch_fast<false, FEpiAccF32<true>>(q, qa, qb, LaunchCfg{0, splits}, s)) return rc;
+    const int rc = fast_ok(q, qa, qb, false)
+                       ? dispatch_fast<false, FEpiAccF32<true>>(q, qa, qb, LaunchCfg{0, splits}, s)
+                       : dispatch<kMaskMM, WS_TILE_ARGS_LARGE, false, EpiAccF32<true>>(
+                             q, qa, qb, LaunchCfg{0, splits}, s);
+    if (rc) return rc;
     const long total = c.r * d;
     hipLaunchKernelGGL(splitk_bf16_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
                        partials, splits, (long)(chunk * d), out, ld_out, (int)c.r, (int)d, skip);
     return hip_check(hipGetLastError(), "split-K reduce launch");
   }
+  q.vec_out = (d % 4 == 0) && (ld_out % 4 == 0) && (reinterpret_cast<unsigned long>(out) % 8 == 0);
   q.c = out;
   q.ldc = ld_out;
-  if (fast) return dispatch_fast<false, FEpiStore<false, false>>(q, qa, qb, kFusedCfg, s);
+  if (fast_ok(q, qa, qb, false)) return dispatch_fast<false, FEpiStore<false, false>>(q, qa, qb, kFusedCfg, s);
   return dispatch<kMaskMM, WS_TILE_ARGS_LARGE, false, EpiStore<false, false>>(q, qa, qb,
                                                                              LaunchCfg{0, 1}, s);
 }
