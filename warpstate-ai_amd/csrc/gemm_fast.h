@@ -666,12 +666,21 @@ struct FEpiCEGrad {
       const float scale = (tgt == -100) ? 0.0f : *p.grad_scale;
       const u32x4_t vl = *reinterpret_cast<const u32x4_t*>(stage + r * kFStageRow + c8 * 2);
       u32x4_t o;
+      // The one-hot term only where some lane of the wave holds its row's target among
+      // its 8 columns (for 4 rows x 128 columns of a 32768 vocabulary, 1 in 64); elsewhere
+      // the term is 0 and x - 0 = x.
+      if (__builtin_amdgcn_ballot_w64(tgt >= n && tgt < n + 8) != 0) {
 #pragma unroll
-      for (int d = 0; d < 4; ++d) {
-        const long e = n + 2 * d;
-        const float v0 = scale * exp_e(lo_bf16(vl[d]) - lse) - (e == tgt ? scale : 0.0f);
-        const float v1 = scale * exp_e(hi_bf16(vl[d]) - lse) - (e + 1 == tgt ? scale : 0.0f);
-        o[d] = pack_bf16x2(v0, v1);
+        for (int d = 0; d < 4; ++d) {
+          const long e = n + 2 * d;
+          const float v0 = scale * exp_e(lo_bf16(vl[d]) - lse) - (e == tgt ? scale : 0.0f);
+          const float v1 = scale * exp_e(hi_bf16(vl[d]) - lse) - (e + 1 == tgt ? scale : 0.0f);
+          o[d] = pack_bf16x2(v0, v1);
+        }
+      } else {
+#pragma unroll
+        for (int d = 0; d < 4; ++d)
+          o[d] = pack_bf16x2(scale * exp_e(lo_bf16(vl[d]) - lse), scale * exp_e(hi_bf16(vl[d]) - lse));
       }
       const long off = (long)r * p.ldc + c8;
       if (full) {
