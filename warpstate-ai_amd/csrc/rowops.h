@@ -149,11 +149,13 @@ static __global__ void __launch_bounds__(256) rmsnorm_fwd_kernel(const unsigned 
 // one partial weight-gradient row (summed across its waves in LDS).
 constexpr int kRmsRowsPerBlock = 32;
 
-template <int SEGS>
+// EAGER (the rounding mode) is a template argument: tested at run time, the compiler computes
+// every element both ways and selects.
+template <int SEGS, bool EAGER>
 static __global__ void __launch_bounds__(256) rmsnorm_bwd_kernel(
     const unsigned short* __restrict__ x, const float* __restrict__ w,
     const float* __restrict__ rstd, const unsigned short* __restrict__ dy,
-    unsigned short* __restrict__ dx, float* __restrict__ dw_part, int rows, int D, int eager) {
+    unsigned short* __restrict__ dx, float* __restrict__ dw_part, int rows, int D) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   float wb[SEGS][8];
 #pragma unroll
@@ -162,7 +164,7 @@ static __global__ void __launch_bounds__(256) rmsnorm_bwd_kernel(
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const float v = c + e < D ? w[c + e] : 0.0f;
-      wb[s][e] = eager ? rbf16(v) : v;
+      wb[s][e] = EAGER ? rbf16(v) : v;
     }
   }
   float part[SEGS][8];
@@ -191,12 +193,20 @@ static __global__ void __launch_bounds__(256) rmsnorm_bwd_kernel(
     for (int s = 0; s < SEGS; ++s) { xv[s] = xn[s]; gv[s] = gn[s]; }
     load(row + 4, xn, gn);
     float dr = 0.0f;
+    // dy * w (rounded when EAGER), kept for the second pass up to 4096 columns (wider rows
+    // recompute it: their registers are spent on the row itself).
+    constexpr bool kKeep = SEGS <= 8;
+    float dz[kKeep ? SEGS : 1][8];
 #pragma unroll
     for (int s = 0; s < SEGS; ++s) {
 #pragma unroll
       for (int d = 0; d < 4; ++d) {
         float dz0 = lo_bf16(gv[s][d]) * wb[s][2 * d], dz1 = hi_bf16(gv[s][d]) * wb[s][2 * d + 1];
-        if (eager) { dz0 = rbf16(dz0); dz1 = rbf16(dz1); }
+        if (EAGER) { dz0 = rbf16(dz0); dz1 = rbf16(dz1); }
+        if constexpr (kKeep) {
+          dz[s][2 * d] = dz0;
+          dz[s][2 * d + 1] = dz1;
+        }
         dr += dz0 * lo_bf16(xv[s][d]);
         dr += dz1 * hi_bf16(xv[s][d]);
       }
@@ -214,13 +224,18 @@ static __global__ void __launch_bounds__(256) rmsnorm_bwd_kernel(
         for (int h = 0; h < 2; ++h) {
           const float xs = h ? hi_bf16(xv[s][d]) : lo_bf16(xv[s][d]);
           const float gs = h ? hi_bf16(gv[s][d]) : lo_bf16(gv[s][d]);
-          float dz = gs * wb[s][2 * d + h];
-          if (eager) dz = rbf16(dz);
-          v2[h] = dz * r + dsq * (2.0f * xs);
+          float dzh;
+          if constexpr (kKeep) {
+            dzh = dz[s][2 * d + h];
+          } else {
+            dzh = gs * wb[s][2 * d + h];
+            if (EAGER) dzh = rbf16(dzh);
+          }
+          v2[h] = dzh * r + dsq * (2.0f * xs);
           float z = xs * r;
-          if (eager) z = rbf16(z);
+          if (EAGER) z = rbf16(z);
           float pv = gs * z;
-          if (eager) pv = rbf16(pv);
+          if (EAGER) pv = rbf16(pv);
           part[s][2 * d + h] += pv;
         }
         o[d] = pack_bf16x2(v2[0], v2[1]);

@@ -62,13 +62,15 @@ template <int SEGS>
 static int launch_rms_bwd(const void* x, const float* weight, const float* rstd, const void* grad,
                           void* dx, float* partial, int rows, int d, int eager, hipStream_t s) {
   const int lds = 4 * d * (int)sizeof(float);
-  const void* kern = reinterpret_cast<const void*>(&rmsnorm_bwd_kernel<SEGS>);
-  if (int rc = ensure_lds(kern, lds)) return rc;
-  hipLaunchKernelGGL(rmsnorm_bwd_kernel<SEGS>, dim3(cdiv(rows, kRmsRowsPerBlock)), dim3(256), lds, s,
-                     static_cast<const unsigned short*>(x), weight, rstd,
-                     static_cast<const unsigned short*>(grad), static_cast<unsigned short*>(dx),
-                     partial, rows, d, eager);
-  return hip_check(hipGetLastError(), "rmsnorm backward launch");
+  auto launch = [&](auto kernel) {
+    if (int rc = ensure_lds(reinterpret_cast<const void*>(kernel), lds)) return rc;
+    hipLaunchKernelGGL(kernel, dim3(cdiv(rows, kRmsRowsPerBlock)), dim3(256), lds, s,
+                       static_cast<const unsigned short*>(x), weight, rstd,
+                       static_cast<const unsigned short*>(grad), static_cast<unsigned short*>(dx),
+                       partial, rows, d);
+    return hip_check(hipGetLastError(), "rmsnorm backward launch");
+  };
+  return eager ? launch(&rmsnorm_bwd_kernel<SEGS, true>) : launch(&rmsnorm_bwd_kernel<SEGS, false>);
 }
 
 static int rmsnorm_backward(const void* x, const float* weight, const float* rstd,
