@@ -143,8 +143,8 @@ def gpu_inputs(m, device):
 
 
 def run_step(inp, out, dp, timer=None):
-    """One hot-path pass on the current stream: every kernel launches through the C ABI,
-    except the two plain input-gradient GEMMs, which run on hipBLASLt (``dgrad_mm``).
+    """One hot-path pass on the current stream: every kernel is this library's and
+    launches through the C ABI.
 
     ``dp`` is this step's incoming gradient of the input projection's output. The QKV
     backward applies the gate-sigmoid backward to it in place (rmsnorm_gate_mm_backward
@@ -237,22 +237,26 @@ def bench_gpu(args):
         kernels[name] = {"ms": round(ms, 4), "tflops": round(f / ms / 1e9, 1),
                          "pct_peak": round(100 * f / ms / 1e9 / PEAK_BF16_TFLOPS, 2),
                          "flops": f}
-    # This library's own GEMM for the two input-gradient products, which the step runs on
-    # hipBLASLt (dgrad_mm): the same weight transpose, then ws_mm, timed the same way.
-    from ops.fused_execution import mm
+    # hipBLASLt (torch.mm) on the same two input-gradient products, as a yardstick for
+    # this library's plain GEMM: the same weight transpose, then the vendor GEMM, timed
+    # the same way. Not part of the step.
+    from ops.fused_execution import k_contiguous_b
 
-    own = Timer()
+    vendor = Timer()
+    for _ in range(max(2, args.warmup)):  # hipBLASLt picks its kernel on a shape's first call
+        torch.mm(out["dpacked"], k_contiguous_b(inp["mlp_w_upgate"], m))
+        torch.mm(inp["qkv_dp"], k_contiguous_b(inp["qkv_w"], m))
     for _ in range(args.steps):
-        with own.region("mlp_bwd.dx"):
-            mm(out["dpacked"], inp["mlp_w_upgate"])
-        with own.region("qkv_bwd.dx"):
-            mm(inp["qkv_dp"], inp["qkv_w"])
+        with vendor.region("mlp_bwd.dx"):
+            torch.mm(out["dpacked"], k_contiguous_b(inp["mlp_w_upgate"], m))
+        with vendor.region("qkv_bwd.dx"):
+            torch.mm(inp["qkv_dp"], k_contiguous_b(inp["qkv_w"], m))
     torch.cuda.synchronize()
     for name in ("mlp_bwd.dx", "qkv_bwd.dx"):
-        ms, f = own.mean_ms(name), sub[name]
-        kernels[name + ".own_gemm"] = {"ms": round(ms, 4), "tflops": round(f / ms / 1e9, 1),
-                                       "pct_peak": round(100 * f / ms / 1e9 / PEAK_BF16_TFLOPS, 2),
-                                       "flops": f}
+        ms, f = vendor.mean_ms(name), sub[name]
+        kernels[name + ".hipblaslt"] = {"ms": round(ms, 4), "tflops": round(f / ms / 1e9, 1),
+                                        "pct_peak": round(100 * f / ms / 1e9 / PEAK_BF16_TFLOPS, 2),
+                                        "flops": f}
     # The RMSNorm row pass of qkv_fwd (HBM-bound): x read once, the normalized rows y and
     # rstd written. The eager standalone forward launches the same kernel
     # (rmsnorm_rows_reg_kernel) as rmsnorm_gate_mm's row pass.
@@ -414,18 +418,36 @@ def cpu_model() -> str:
     return platform.processor() or platform.machine()
 
 
+def _median_seconds(fn, min_runs=3, budget_s=4.0, max_runs=10):
+    """Median wall time of ``fn`` over at least ``min_runs`` runs after one warmup, more
+    while ``budget_s`` lasts."""
+    fn()
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < min_runs or (time.perf_counter() - t_start < budget_s
+                                    and len(times) < max_runs):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    return times[len(times) // 2]
+
+
 def cpu_baseline(rows):
-    """The CPU oracle (the reference's eager PyTorch path restated) on `rows` tokens of the
-    same step; returns (TFLOP/s, seconds per step, threads)."""
+    """The CPU oracle (the reference's eager PyTorch path restated, BF16 CPU tensors) on
+    the host's cores: the layer step on a ``rows``-token sample, and each of the five
+    configurations, config 1 at its full size and configs 2-5 on a ``rows``-row sample of
+    their 16384 rows (every GEMM row, and every loss row, depends only on its own input
+    row, so throughput per row is the same). Returns (step TFLOP/s, step seconds, threads,
+    per-config dict)."""
     from oracle import reference as oracle
-    from ops.benchmark_configs import (down_residual_inputs, mlp_backward_inputs,
-                                       rms_projection_inputs)
+    from ops import benchmark_configs as cfg
 
     threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or os.cpu_count() or 1
     torch.set_num_threads(threads)
-    qkv = rms_projection_inputs(m=rows, d=D, n=NQKV, gate=GATE, seed=0)
-    down = down_residual_inputs(m=rows, ffn=FFN, d=D, seed=0)
-    mlp = mlp_backward_inputs(m=rows, d=D, ffn=FFN, seed=0)
+    qkv = cfg.rms_projection_inputs(m=rows, d=D, n=NQKV, gate=GATE, seed=0)
+    down = cfg.down_residual_inputs(m=rows, ffn=FFN, d=D, seed=0)
+    mlp = cfg.mlp_backward_inputs(m=rows, d=D, ffn=FFN, seed=0)
     gen = torch.Generator("cpu").manual_seed(1)
     dp = (torch.randn((rows, NQKV), generator=gen) * 1e-2).bfloat16()
     g_qkv = torch.randn((NQKV, D), generator=gen) * 1e-4
@@ -439,16 +461,39 @@ def cpu_baseline(rows):
         oracle.rmsnorm_gate_projection_backward(qkv["x"], qkv["norm_weight"], qkv["eps"],
                                                 qkv["w"], GATE, dp, g_qkv)
 
-    step()  # warmup
-    times = []
-    t_start = time.perf_counter()
-    while len(times) < 3 or (time.perf_counter() - t_start < 10 and len(times) < 20):
-        t0 = time.perf_counter()
-        step()
-        times.append(time.perf_counter() - t0)
-    times.sort()
-    sec = times[len(times) // 2]
-    return sum(flops_step(rows).values()) / sec / 1e12, sec, torch.get_num_threads()
+    sec = _median_seconds(step, budget_s=10.0, max_runs=20)
+    step_tflops = sum(flops_step(rows).values()) / sec / 1e12
+
+    c1 = cfg.swiglu_forward_inputs(seed=0)
+    packed, act = oracle.swiglu_mm(mlp["x"], mlp["w_upgate"].T, True)
+    lm = cfg.lm_head_inputs(m=rows, seed=0)
+    cases = {
+        "config1_swiglu_4096x1024x5632": (
+            4096, cfg.flops_swiglu_forward(4096, 1024, 2816),
+            lambda: oracle.swiglu_mm(c1["x"], c1["w_upgate"].T, False)),
+        "config2_rmsnorm_qkv_16384x2048x9216": (
+            rows, cfg.flops_rms_projection(rows, D, NQKV),
+            lambda: oracle.rmsnorm_gate_projection(qkv["x"], qkv["norm_weight"], qkv["eps"],
+                                                   qkv["w"], GATE)),
+        "config3_down_residual_16384x5632x2048": (
+            rows, cfg.flops_down_residual(rows, FFN, D),
+            lambda: oracle.residual_projection(down["h"], down["w_down"], down["residual"])),
+        "config4_mlp_backward_16384x2048x5632": (
+            rows, cfg.flops_mlp_backward(rows, D, FFN),
+            lambda: oracle.mlp_backward(mlp["x"], mlp["w_upgate"], mlp["w_down"], packed, act,
+                                        mlp["dy"], mlp["g_upgate"], mlp["g_down"])),
+        "config5_lm_head_ce_16384x2048x32768": (
+            rows, cfg.flops_lm_head(rows, D, VOCAB),
+            lambda: oracle.linear_cross_entropy(lm["hidden"], lm["weight"], lm["targets"])),
+    }
+    per_config = {}
+    for name, (sample_rows, flops, fn) in cases.items():
+        t = _median_seconds(fn)
+        per_config[name] = {"ms": round(t * 1e3, 2), "tflops": round(flops / t / 1e12, 4),
+                            "rows": sample_rows,
+                            "sample": "full size" if name.startswith("config1")
+                            else f"{sample_rows} of 16384 rows"}
+    return step_tflops, sec, torch.get_num_threads(), per_config
 
 
 TRAFFIC_PROFILE = ROOT / "profiles" / "hbm_traffic_layer_step_m16384.md"
@@ -496,31 +541,38 @@ def main():
         hbm.update(per_config.pop("_hbm"))
         hbm["attention_bwd_layout_4x16x32x128x64"] = bench_layout(args, device)
     value = step_flops / wall_ms / 1e9
-    # The dominant kernel of the step (the own-GEMM comparison lines are not in the step).
-    dom_name = max((k for k in kernels if not k.endswith(".own_gemm")),
+    # The dominant kernel of the step (the hipBLASLt yardstick lines are not in the step).
+    dom_name = max((k for k in kernels if not k.endswith(".hipblaslt")),
                    key=lambda k: kernels[k]["ms"])
     dom = kernels[dom_name]
     roofline = {"bound": "mfma", "kernel": dom_name,
                 "achieved": round(dom["flops"] / dom["ms"] / 1e9, 1),
                 "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                 "frac": round(dom["flops"] / dom["ms"] / 1e9 / PEAK_BF16_TFLOPS, 4),
-                "traffic": measured_traffic(dom_name)}
+                "frac_source": "HIP events around each launch of the region in this run",
+                "traffic": measured_traffic(dom_name),
+                "traffic_source": f"profiles/{TRAFFIC_PROFILE.name} (rocprofv3 FETCH_SIZE + "
+                                  "WRITE_SIZE, committed; not measured in this run)"}
     # The same region's kernels in the committed rocprofv3 trace (sum of their average
     # durations), for comparison with the HIP-event figure above.
     trace_us = _profile_value(TRACE_PROFILE, "trace_us", dom_name)
     if trace_us:
+        roofline["trace_source"] = (f"profiles/{TRACE_PROFILE.name} (rocprofv3 kernel trace, "
+                                    "committed; not measured in this run)")
         roofline["trace_us"] = trace_us
         roofline["trace_achieved"] = round(dom["flops"] / trace_us / 1e6, 1)
         roofline["trace_frac"] = round(dom["flops"] / trace_us / 1e6 / PEAK_BF16_TFLOPS, 4)
     cpu = None
     if not args.no_cpu:
-        tflops, sec, threads = cpu_baseline(args.cpu_rows)
+        tflops, sec, threads, per_config_cpu = cpu_baseline(args.cpu_rows)
         cpu = {"value": round(tflops, 4), "unit": "TFLOP/s", "cores": threads,
                "kind": "port",
                "sample": f"the same step at M={args.cpu_rows} tokens (of {args.rows}), "
-                         f"median of >=3 runs, {sec:.2f} s/step",
+                         f"median of >=3 runs, {sec:.2f} s/step; per_config: each "
+                         f"configuration's oracle path, config 1 in full, configs 2-5 on "
+                         f"{args.cpu_rows} of their 16384 rows",
                "cpu_model": cpu_model(), "os_cpu_count": os.cpu_count(),
-               "torch_threads": threads}
+               "torch_threads": threads, "per_config": per_config_cpu}
     line = {"metric": METRIC, "value": round(value, 1), "unit": "TFLOP/s", "n_gpus": 1,
             "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(wall_ms, 4),
             "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",

@@ -92,8 +92,9 @@ int ws_rmsnorm_backward(const void* x, const float* weight, const float* rstd, c
  * weight-gradient partials in a static 4 MiB device array of the library instead of a
  * caller workspace. No counterpart in the reference: it is for callers that cannot
  * allocate (code under HIP graph capture, tight serving loops, harnesses that forbid
- * hipMalloc). It calls no allocator. Limit: ceil(rows / 32) * d <=
- * ws_rmsnorm_backward_static_max_partial_floats() (2^20; e.g. 16384 x 2048), larger
+ * hipMalloc). It calls no allocator. Limits: d <= 4096 (wider rows take a kernel that
+ * spills to runtime-allocated private memory) and ceil(rows / 32) * d <=
+ * ws_rmsnorm_backward_static_max_partial_floats() (2^20; e.g. 16384 x 2048); larger
  * sizes return an error. Each GPU holds its own copy of the array until the process
  * ends; calls that overlap on one GPU share it and race. */
 int ws_rmsnorm_backward_static(const void* x, const float* weight, const float* rstd,
@@ -267,11 +268,12 @@ int ws_linear_ce_fused(const void* hidden, int64_t ld_hidden, const void* weight
 /*
  * Backward of ws_linear_ce_fused for the actual upstream gradient grad_mean (device FP32
  * scalar): dhidden [rows, d] BF16 (row stride ld_dhidden) and, when given, dweight
- * [vocab, d] FP32 (contiguous, +=). When grad_mean is a power of two, scaling commutes with
- * every rounding, and the results are grad_mean * dhidden_unit and dweight + grad_mean *
- * dweight_unit: the two-pass backward's results bit for bit (dweight up to summation order
- * into a nonzero buffer). Otherwise it runs the two-pass backward (ws_linear_ce_backward's
- * arguments). The choice is made on the device, without a host synchronisation: both paths
+ * [vocab, d] FP32 (contiguous, +=). When grad_mean is +-2^e with |e| <= 32, scaling
+ * commutes with every rounding that stays in the normal range, and the results are
+ * grad_mean * dhidden_unit and dweight + grad_mean * dweight_unit: the two-pass backward's
+ * results bit for bit (dweight up to summation order into a nonzero buffer), except for
+ * elements that are subnormal before or after the scaling. Otherwise it runs the two-pass
+ * backward (ws_linear_ce_backward's arguments). The choice is made on the device, without a host synchronisation: both paths
  * are launched and the kernels of the one not taken exit at once.
  */
 int ws_linear_ce_fused_backward(const void* hidden, int64_t ld_hidden, const void* weight,

@@ -132,3 +132,13 @@ def test_grouped_fallback_splits_follow_auto_splits():
             want = max(_hip.query("ws_mm_accumulate_workspace_floats", m, n, k,
                                   auto_splits(m, n, k, cus)) for m, n in shapes)
             assert _hip.query("ws_mm_accumulate_group_workspace_floats", rows, len(shapes), k) == want
+
+
+def test_static_rmsnorm_backward_refuses_wide_rows_before_any_launch():
+    """The allocation-free RMSNorm backward takes rows of at most 4096 columns: wider rows
+    need a kernel that spills to private memory the runtime would allocate. The check runs
+    before any device call."""
+    gpu_ptr = 1 << 20  # never dereferenced
+    with pytest.raises(RuntimeError, match="at most 4096 columns"):
+        _hip.call("ws_rmsnorm_backward_static", gpu_ptr, gpu_ptr, gpu_ptr, gpu_ptr, gpu_ptr,
+                  gpu_ptr, 8, 4104, 1, None)

@@ -67,17 +67,47 @@ def test_config3_down_residual_full():
     assert torch.equal(same, r)
 
 
-def test_config4_mlp_backward_full():
+def test_swiglu_forward_m16384_persistent_full():
+    """The paired SwiGLU forward at the layer's training shape, X [16384, 2048] against
+    W_upgate [11264, 2048], on the persistent grid (as the bench step and the training
+    adapter run it): packed and act on 512 spread rows against the oracle, and zero
+    weights give exact zeros everywhere."""
+    from ops.matmul_epilogue import launch_swiglu_mm
+
+    inp = cfg.mlp_backward_inputs(seed=0)
+    x, wug = inp["x"].cuda(), inp["w_upgate"].cuda()
+    packed, act = launch_swiglu_mm(x, wug.T, "persistent", (128, 128, 32, 8, 3), True)
+    torch.cuda.synchronize()
+    assert packed.shape == (16384, 11264) and act.shape == (16384, 5632)
+    want_packed, want_act = oracle.swiglu_mm(inp["x"][SAMPLE], inp["w_upgate"].T, True)
+    rows = SAMPLE.cuda()
+    assert_bf16_close(packed[rows], want_packed, "M=16384 persistent packed sample rows")
+    assert_bf16_close(act[rows], want_act, "M=16384 persistent act sample rows")
+    zp, za = launch_swiglu_mm(x, torch.zeros_like(wug).T, "persistent", (128, 128, 32, 8, 3), True)
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(zp).item() == 0 and torch.count_nonzero(za).item() == 0
+
+
+def test_config4_mlp_backward_full(monkeypatch):
+    """Config 4 in full on this library's kernels only: the dAct GEMM with the SwiGLU
+    backward epilogue, the input gradient dX on the library's GEMM (ws_mm) and both weight
+    gradients in one grouped FP32-accumulating launch, each against the oracle."""
+    from ops import _hip
     from ops.fused_execution import mlp_backward
     from ops.matmul_epilogue import launch_swiglu_mm
 
     inp = cfg.mlp_backward_inputs(seed=0)
     x, wug, wd, dy = (inp[k].cuda() for k in ("x", "w_upgate", "w_down", "dy"))
     g_up, g_down = inp["g_upgate"].cuda(), inp["g_down"].cuda()
-    packed, act = launch_swiglu_mm(x, wug.T, "tiled", (128, 128, 32, 8, 3), True)
+    packed, act = launch_swiglu_mm(x, wug.T, "persistent", (128, 128, 32, 8, 3), True)
     dpacked = torch.empty_like(packed)
+    calls, real = [], _hip.call
+    monkeypatch.setattr(_hip, "call", lambda name, *a: (calls.append(name), real(name, *a))[1])
     dx = mlp_backward(x, wug, wd, packed, act, dy, g_up, g_down, dpacked=dpacked)
     torch.cuda.synchronize()
+    monkeypatch.setattr(_hip, "call", real)
+    assert calls == ["ws_transpose_bf16", "ws_swiglu_backward_mm", "ws_transpose_bf16", "ws_mm",
+                     "ws_mm_accumulate_f32_group"], calls
     # The oracle consumes the same saved forward tensors (they are parity-checked in the
     # forward tests), so the backward is compared on identical inputs.
     want_dx, want_dpacked, want_up, want_down = oracle.mlp_backward(

@@ -140,10 +140,9 @@ def test_lm_head_cross_entropy_replays_bitwise_under_graph_capture(mode):
 
 @pytest.mark.parametrize("m,n,k", [(16384, 11264, 2048), (16384, 9216, 2048), (512, 768, 256)])
 def test_input_gradient_gemm_replays_bitwise_under_graph_capture(m, n, k):
-    """dgrad_mm (the weight transpose, then hipBLASLt) captured once at the layer's shapes
-    and replayed three times with other work and a cleared output between replays: every
-    replay equals the eager call bit for bit. hipBLASLt's stream-K kernel for these shapes
-    clears its workspace with a fill before each launch, which the graph records."""
+    """dgrad_mm (the weight transpose, then this library's GEMM) captured once at the
+    layer's shapes and replayed three times with other work and a cleared output between
+    replays: every replay equals the eager call bit for bit."""
     from ops.fused_execution import dgrad_mm
 
     g = torch.Generator().manual_seed(m + n)

@@ -27,7 +27,8 @@ namespace ws {
 // forward. Rows of at most 4096 vector-aligned features stay in registers (x read once).
 int launch_rmsnorm_rows(const void* x, long ldx, const float* w, void* y, float* rstd, long m,
                         long k, float eps, hipStream_t s) {
-  const int vec = (ldx % 8 == 0) && (k % 8 == 0) && al(x, 16) && al(y, 16);
+  // The vector kernels read x and the FP32 weight, and write y, as 16-byte pieces.
+  const int vec = (ldx % 8 == 0) && (k % 8 == 0) && al(x, 16) && al(y, 16) && al(w, 16);
   const dim3 grid(cdiv(m, 4));
   const auto* xs = static_cast<const unsigned short*>(x);
   auto* ys = static_cast<unsigned short*>(y);

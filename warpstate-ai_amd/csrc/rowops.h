@@ -524,15 +524,18 @@ static __global__ void __launch_bounds__(256) scale_add_f32_kernel(const float* 
   if (i < n) acc[i] += *g * x[i];
 }
 
-// exact[0] = 1 when g is a positive or negative power of two (a normal FP32 number with an
-// all-zero mantissa): scaling by g then commutes with every BF16 and FP32 rounding of the
-// LM-head gradients, so the fused pass's unit gradients scaled by g are the gradients the
-// two-pass backward computes for g, bit for bit.
+// exact[0] = 1 when g is +-2^e with |e| <= 32 (a normal FP32 number with an all-zero
+// mantissa, exponent within 32 of 1): scaling by g then commutes with every BF16 and FP32
+// rounding of the LM-head gradients that stays in the normal range, so the fused pass's
+// unit gradients scaled by g are the gradients the two-pass backward computes for g, bit
+// for bit, except for elements that are subnormal before or after the scaling (where
+// r(g r(x)) and r(g x) can differ). The window keeps the scaled gradients of ordinary
+// magnitude normal and far from overflow; other values take the two-pass backward.
 static __global__ void ce_exact_scale_kernel(const float* __restrict__ g, int* __restrict__ exact) {
   if (threadIdx.x == 0) {
     const unsigned bits = __float_as_uint(g[0]);
-    const unsigned expo = (bits >> 23) & 0xff;
-    exact[0] = (bits & 0x7fffff) == 0 && expo != 0 && expo != 0xff;
+    const int expo = (int)((bits >> 23) & 0xff) - 127;
+    exact[0] = (bits & 0x7fffff) == 0 && expo >= -32 && expo <= 32;
   }
 }
 

@@ -117,6 +117,7 @@ extern "C" int ws_rmsnorm_backward(const void* x, const float* weight, const flo
 namespace {
 
 constexpr long kStaticPartialFloats = 1L << 20;  // 4 MiB: rows x d up to 2^25 at d % 8 == 0
+constexpr int kStaticMaxWidth = 4096;  // the widest row of a spill-free kernel (8 segments)
 __device__ __align__(256) float scratch[kStaticPartialFloats];
 
 constexpr int kScratchDevices = 64;
@@ -152,6 +153,13 @@ extern "C" int ws_rmsnorm_backward_static(const void* x, const float* weight, co
                                           void* stream) {
   if (rows < 1 || d < 1 || !fits_i32(rows) || !fits_i32(d))
     return set_error(kInvalid, "invalid RMSNorm shape");
+  // Rows wider than 4096 take the 16-segment kernel, which spills registers to private
+  // scratch memory that the HIP runtime would have to allocate.
+  if (d > kStaticMaxWidth)
+    return set_error(kInvalid,
+                     "the allocation-free RMSNorm backward takes rows of at most %d columns "
+                     "(got %ld; use ws_rmsnorm_backward)",
+                     kStaticMaxWidth, (long)d);
   const long need = ws_rmsnorm_backward_partial_floats(rows, d);
   if (need > kStaticPartialFloats)
     return set_error(kInvalid,

@@ -16,7 +16,9 @@ prologue or epilogue does the extra work in registers:
 * ``mm_accumulate_``: weight-gradient GEMM accumulated into an FP32 buffer,
   G += f32(r(dW)) (test_gradient_execution.py:243-246).
 * ``linear_cross_entropy_*``: the tied LM head with fused cross-entropy
-  (warpstate/model.py:316-334, ops/loss_experiment.py:14-19); logits never reach HBM.
+  (warpstate/model.py:316-334, ops/loss_experiment.py:14-19); the full [rows, vocab]
+  logits never exist in HBM (the two-pass mode keeps them in registers only; the one-pass
+  mode holds one row chunk's BF16 logits in its workspace at a time).
 * ``mlp_backward``: the SwiGLU MLP backward at training shape built from the above.
 """
 
@@ -102,17 +104,14 @@ def dgrad_mm(grad: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
     gradient) and the BF16 weight [N, K] in nn.Linear layout; returns [M, K]
     (ops/matmul_execution.py:239).
 
-    A plain GEMM, so it runs on hipBLASLt (``torch.mm``): with the weight first copied
-    K-contiguous by the HIP transpose kernel (``k_contiguous_b``), hipBLASLt's kernel for
-    that layout is 16-18 % faster than this library's GEMM at the layer's input-gradient
-    shapes (16384 x 2048 x 9216 and x 11264) and gives the same bits there (FP32
-    accumulation, one BF16 rounding). ``mm`` keeps this library's kernel for the same
-    product.
+    This library's GEMM (``ws_mm``, FP32 accumulation, one BF16 rounding), with the
+    weight first copied K-contiguous by the HIP transpose kernel (``k_contiguous_b``) when
+    grad has enough rows to amortize the copy.
     """
     _check_bf16_cuda(grad, weight)
     if grad.dim() != 2 or weight.dim() != 2 or grad.shape[1] != weight.shape[0]:
         raise ValueError("Expected grad [M, N] and weight [N, K]")
-    return torch.mm(grad, k_contiguous_b(weight, grad.shape[0]))
+    return mm(grad, weight)
 
 
 def rmsnorm_gate_mm(x: torch.Tensor, norm_weight: torch.Tensor, eps: float,
@@ -509,17 +508,27 @@ class LinearCrossEntropy(torch.autograd.Function):
     rounded to BF16 first, as F.linear under BF16 autocast does. The weight's gradient is
     accumulated in FP32 chunk by chunk, sum_c f32(r(G_c^T h_c)); an FP32 weight (the
     master parameter) receives that FP32 sum, a BF16 weight its BF16 rounding. The
-    per-token loss is not differentiable."""
+    per-token loss is not differentiable.
+
+    ``mode`` picks how the gradients are formed when they are needed:
+    ``"fused"`` (default) computes them in the forward for a unit upstream gradient, while
+    each chunk's logits are at hand (one logits GEMM per row), and the backward scales them;
+    that is exact for an upstream gradient 2^e with |e| <= 32. Any other upstream gradient
+    (for example a loss divided by 3 microbatches) makes the backward run the two-pass
+    backward on top, a second logits GEMM plus the dHidden and weight GEMMs again, about
+    twice the LM head's cost. ``"two_pass"`` keeps only row statistics in the forward and
+    always recomputes the logits in the backward: the right choice when such upstream
+    gradients are expected."""
 
     @staticmethod
-    def forward(ctx, hidden, weight, targets, chunk_rows=DEFAULT_CE_CHUNK_ROWS):
+    def forward(ctx, hidden, weight, targets, chunk_rows=DEFAULT_CE_CHUNK_ROWS, mode="fused"):
+        if mode not in ("fused", "two_pass"):
+            raise ValueError(f"mode must be 'fused' or 'two_pass', not {mode!r}")
         h, w = _bf16_rows(hidden), _bf16_rows(weight)
-        # With gradients to come, the fused pass computes them for a unit upstream gradient
-        # while it has each chunk's logits (one logits GEMM per row); the backward only
-        # scales them.
         wants = ctx.needs_input_grad
+        fused = mode == "fused" and (wants[0] or wants[1])
         state = CrossEntropyState(h.shape[0], w.shape[0], h.device, chunk_rows, d=h.shape[1],
-                                  fused=wants[0] or wants[1], weight_grad=wants[1])
+                                  fused=fused, weight_grad=fused and wants[1])
         linear_cross_entropy_forward(h, w, targets, state)
         ctx.save_for_backward(h, w, targets)
         ctx.state = state
@@ -539,14 +548,16 @@ class LinearCrossEntropy(torch.autograd.Function):
                                            weight_grad=weight_grad)
         hidden_dtype, weight_dtype = ctx.dtypes
         return (dh.to(hidden_dtype) if want_h else None,
-                weight_grad.to(weight_dtype) if want_w else None, None, None)
+                weight_grad.to(weight_dtype) if want_w else None, None, None, None)
 
 
 @torch.compiler.disable
-def linear_cross_entropy(hidden, weight, targets, chunk_rows=DEFAULT_CE_CHUNK_ROWS):
-    """(mean, per-token loss) of the fused LM head, with autograd to hidden and weight.
-    Under torch.compile it runs eagerly (a graph break), with its own buffers."""
-    return LinearCrossEntropy.apply(hidden, weight, targets, chunk_rows)
+def linear_cross_entropy(hidden, weight, targets, chunk_rows=DEFAULT_CE_CHUNK_ROWS,
+                         mode="fused"):
+    """(mean, per-token loss) of the fused LM head, with autograd to hidden and weight
+    (``mode``: see ``LinearCrossEntropy``). Under torch.compile it runs eagerly (a graph
+    break), with its own buffers."""
+    return LinearCrossEntropy.apply(hidden, weight, targets, chunk_rows, mode)
 
 
 def mlp_backward(x: torch.Tensor, w_upgate: torch.Tensor, w_down: torch.Tensor,

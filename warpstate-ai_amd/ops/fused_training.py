@@ -10,7 +10,8 @@ core and of the loss that the fused kernels of ``ops.fused_execution`` cover:
   the SwiGLU block with its residual add (warpstate/model.py:52-60, :178) become
   ``residual_mm`` and ``launch_swiglu_mm`` + ``residual_mm``;
 * the chunked tied-head loss (warpstate/model.py:316-334) becomes the fused
-  cross-entropy (``linear_cross_entropy``), whose logits never reach HBM.
+  cross-entropy (``linear_cross_entropy``), which never holds the full [rows, vocab]
+  logits in HBM (one row chunk's BF16 logits at a time in its one-pass mode).
 
 Each core piece is a registered operator (``warpstate::fused_norm_projection``,
 ``warpstate::fused_residual_projection``, ``warpstate::fused_swiglu_block``) with a fake

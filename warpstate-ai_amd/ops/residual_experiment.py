@@ -7,28 +7,48 @@ is BF16: x <- r(x + r(projection)), the arithmetic of the fused residual epilogu
 casts are differentiable, so gradients reach the FP32 masters, and the optimizer, the
 state dict and every other parameter are unchanged. Calls outside BF16 autocast run the
 original forward.
+
+Design: each cast parameter is addressed by its owning module's parameter slot. For the
+duration of one call the slot holds the BF16 cast; a ``finally`` puts the FP32 master
+back, also when the forward raises. No module is added to the model, so the state dict
+keeps its keys.
 """
 
 from __future__ import annotations
 
+from contextlib import contextmanager
+
 import torch
-from torch.func import functional_call
 
-_CAST = ("embed.weight", "depth_scale", "depth_bias")
+# The parameters whose values enter the residual stream (warpstate/model.py: the token
+# embedding, tied with the LM head, and the per-depth scale and bias).
+_STREAM_PARAMETERS = ("embed.weight", "depth_scale", "depth_bias")
 
 
-class _Detached(torch.nn.Module):
-    """Holds the model for ``functional_call`` and runs its original forward. It is kept
-    only by the patched forward's closure, never registered on the model, so the model's
-    state dict keeps its keys."""
+def _slot(model: torch.nn.Module, name: str) -> tuple[torch.nn.Module, str]:
+    """(owning module, attribute) of a dotted parameter name."""
+    owner_name, _, attr = name.rpartition(".")
+    return (model.get_submodule(owner_name) if owner_name else model), attr
 
-    def __init__(self, model: torch.nn.Module, forward):
-        super().__init__()
-        self.model = model
-        self.run = forward
 
-    def forward(self, *args, **kwargs):
-        return self.run(*args, **kwargs)
+@contextmanager
+def _bf16_slots(slots):
+    """Put r(master) into each (module, attribute, master) slot, restore the masters on
+    exit."""
+    try:
+        for module, attr, master in slots:
+            # Written into the parameter table directly: Module.__setattr__ would refuse a
+            # non-Parameter tensor for a registered parameter name.
+            module._parameters[attr] = master.to(torch.bfloat16)
+        yield
+    finally:
+        for module, attr, master in slots:
+            module._parameters[attr] = master
+
+
+def _bf16_autocast(device_type: str) -> bool:
+    return (torch.is_autocast_enabled(device_type)
+            and torch.get_autocast_dtype(device_type) == torch.bfloat16)
 
 
 def apply_bf16_residuals(model: torch.nn.Module) -> None:
@@ -36,23 +56,19 @@ def apply_bf16_residuals(model: torch.nn.Module) -> None:
     and loading weights, before any DDP wrapper."""
     if getattr(model, "_bf16_residuals", False):
         raise ValueError("BF16 residual execution has already been applied")
-    masters = {name: model.get_parameter(name) for name in _CAST}
-    if any(p.dtype != torch.float32 for p in masters.values()):
+    slots = []
+    for name in _STREAM_PARAMETERS:
+        module, attr = _slot(model, name)
+        slots.append((module, attr, module._parameters[attr]))
+    if any(master.dtype != torch.float32 for _, _, master in slots):
         raise ValueError("BF16 residual execution requires FP32 master parameters")
-    original = model.forward
-    holder = _Detached(model, original)
+    unpatched = model.forward
 
     def forward(input_ids, targets=None, *, return_logits=True):
-        kind = input_ids.device.type
-        if not (torch.is_autocast_enabled(kind)
-                and torch.get_autocast_dtype(kind) == torch.bfloat16):
-            return original(input_ids, targets, return_logits=return_logits)
-        # functional_call swaps the casts in for the call and restores the masters after
-        # it, also when the forward raises.
-        casts = {"model." + name: p.to(torch.bfloat16) for name, p in masters.items()}
-        return functional_call(holder, casts, (input_ids,),
-                               {"targets": targets, "return_logits": return_logits},
-                               strict=False)
+        if not _bf16_autocast(input_ids.device.type):
+            return unpatched(input_ids, targets, return_logits=return_logits)
+        with _bf16_slots(slots):
+            return unpatched(input_ids, targets, return_logits=return_logits)
 
     model.forward = forward
     model._bf16_residuals = True
