@@ -257,6 +257,26 @@ def bench_gpu(args):
         kernels[name + ".hipblaslt"] = {"ms": round(ms, 4), "tflops": round(f / ms / 1e9, 1),
                                         "pct_peak": round(100 * f / ms / 1e9 / PEAK_BF16_TFLOPS, 2),
                                         "flops": f}
+    # The training adapter's MLP backward operator on the same tensors: the same kernels
+    # as mlp_bwd, with the two weight gradients written into fresh FP32 buffers (returned
+    # through autograd) instead of accumulated into resident ones.
+    from ops.fused_training import fused_swiglu_block_backward
+    from ops.matmul_epilogue import launch_swiglu_mm
+
+    packed, act = launch_swiglu_mm(inp["mlp_x"], inp["mlp_w_upgate"].T, "persistent",
+                                   (128, 128, 32, 8, 3), True)
+    adapter = Timer()
+    for i in range(args.warmup + args.steps):
+        with adapter.region("run" if i >= args.warmup else "warm"):
+            fused_swiglu_block_backward(inp["mlp_dy"], inp["mlp_x"], packed, act,
+                                        inp["mlp_w_upgate"], inp["mlp_w_down"])
+    torch.cuda.synchronize()
+    f = sub["mlp_bwd.dact_swiglu"] + sub["mlp_bwd.dx"] + sub["mlp_bwd.wgrad"]
+    ms = adapter.mean_ms("run")
+    kernels["mlp_bwd.adapter_op"] = {"ms": round(ms, 4), "tflops": round(f / ms / 1e9, 1),
+                                     "pct_peak": round(100 * f / ms / 1e9 / PEAK_BF16_TFLOPS, 2),
+                                     "flops": f}
+    del packed, act
     # The RMSNorm row pass of qkv_fwd (HBM-bound): x read once, the normalized rows y and
     # rstd written. The eager standalone forward launches the same kernel
     # (rmsnorm_rows_reg_kernel) as rmsnorm_gate_mm's row pass.
@@ -542,7 +562,7 @@ def main():
         hbm["attention_bwd_layout_4x16x32x128x64"] = bench_layout(args, device)
     value = step_flops / wall_ms / 1e9
     # The dominant kernel of the step (the hipBLASLt yardstick lines are not in the step).
-    dom_name = max((k for k in kernels if not k.endswith(".hipblaslt")),
+    dom_name = max((k for k in kernels if not k.endswith((".hipblaslt", ".adapter_op"))),
                    key=lambda k: kernels[k]["ms"])
     dom = kernels[dom_name]
     roofline = {"bound": "mfma", "kernel": dom_name,

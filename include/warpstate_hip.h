@@ -200,6 +200,22 @@ int64_t ws_mm_accumulate_group_workspace_floats(const ws_accumulate_problem* pro
 int ws_mm_accumulate_f32_group(const ws_accumulate_problem* problems, int count, int64_t k,
                                int round_bf16, float* workspace, void* stream);
 
+/*
+ * G = f32(r(A @ B)) (or the FP32 product when round_bf16 is 0): ws_mm_accumulate_f32 and
+ * ws_mm_accumulate_f32_group with the gradient buffers written instead of updated, so
+ * they need no clearing and are never read. Same arguments, workspace sizes
+ * (ws_mm_accumulate_workspace_floats, ws_mm_accumulate_group_workspace_floats) and
+ * paths. This is the BF16 weight gradient of F.linear under autocast widened to FP32,
+ * the value AccumulateGrad adds to an FP32 master's .grad
+ * (ops/matmul_execution.py:243; test_gradient_execution.py:243-246), produced in one
+ * FP32 pass for an adapter that returns it through autograd (new).
+ */
+int ws_mm_store_f32(const void* a, int64_t a_s0, int64_t a_s1, const void* b, int64_t b_s0,
+                    int64_t b_s1, float* g, int64_t ldg, int64_t m, int64_t n, int64_t k,
+                    int round_bf16, float* workspace, int64_t splits, void* stream);
+int ws_mm_store_f32_group(const ws_accumulate_problem* problems, int count, int64_t k,
+                          int round_bf16, float* workspace, void* stream);
+
 /* Number of per-row partials (floats per row of part_max / part_sum) for `vocab`. */
 int64_t ws_linear_ce_parts(int64_t vocab);
 

@@ -327,7 +327,7 @@ def _fused_adapter_case(size, hip_calls):
     # The projection weight's gradient went through autograd (where DDP's hooks sit).
     assert hooked and all(dtype == torch.float32 for dtype in hooked), hooked
     for name in ("ws_linear_ce_fused_backward", "ws_sigmoid_backward_cols", "ws_swiglu_backward_mm",
-                 "ws_mm_accumulate_f32", "ws_rmsnorm_backward"):
+                 "ws_mm_store_f32", "ws_rmsnorm_backward"):
         assert any(call.startswith(name) for call in hip_calls), (name, hip_calls)
     assert math.isclose(result.item(), expected.item(), rel_tol=1e-3)
     for (name, p), q in zip(reference.named_parameters(), actual.parameters(), strict=True):
@@ -348,6 +348,71 @@ def _fused_adapter_case(size, hip_calls):
         logits = actual(inputs)
         assert not hip_calls
         assert logits.shape == (*tokens, vocab)
+
+
+@pytest.mark.parametrize("variant", ["eager", "checkpointed", "compiled_cores"])
+def test_fused_adapter_on_the_reference_core_layout(variant, hip_calls):
+    """A model in the reference's own layout (one WarpStateCore.forward with _split, the
+    inline gate sigmoid and residual adds, and the inline chunked loss; no seams): the
+    adapter attaches its RMSNorm, Linear and SwiGLU modules and the loss (through a forward
+    wrap that stops at final_norm), and loss and every parameter gradient agree with the
+    unpatched model at the reference's bars (loss rtol 1e-3, gradient cosine > 0.999)
+    under BF16 autocast with BF16 residuals. No weight gradient is formed in a cleared
+    buffer: every one comes from the FP32 store GEMMs, through autograd."""
+    from inline_layout_model import InlineLM
+    from warpstate.config import WarpStateConfig
+
+    from ops.fused_training import apply_fused_execution
+    from ops.residual_experiment import apply_bf16_residuals
+
+    try:
+        torch.manual_seed(733)
+        vocab, tokens = 2048, (4, 64)
+        reference = InlineLM(WarpStateConfig(
+            vocab_size=vocab, d_model=256, n_heads=4, n_cores=2, logical_depth=3,
+            ffn_hidden=512, loss_chunk_size=96,
+            gradient_checkpointing=variant == "checkpointed")).train().cuda()
+        actual = copy.deepcopy(reference)
+        keys = tuple(actual.state_dict())
+        apply_fused_execution(actual)
+        for model in (reference, actual):
+            apply_bf16_residuals(model)
+        if variant == "compiled_cores":
+            _compile_training_cores(actual, "aot_eager")
+        gen = torch.Generator("cpu").manual_seed(12)
+        inputs = torch.randint(vocab, tokens, generator=gen).cuda()
+        labels = torch.randint(vocab, tokens, generator=gen)
+        labels.view(-1)[::7] = -100
+        labels = labels.cuda()
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            expected = reference(inputs, labels, return_logits=False)[1]
+            hip_calls.clear()
+            result = actual(inputs, labels, return_logits=False)[1]
+        for name in ("ws_rmsnorm_forward", "ws_mm", "ws_swiglu_mm", "ws_linear_ce_fused"):
+            assert name in hip_calls, (name, hip_calls)
+        # The seams' fusions are not available here.
+        assert "ws_rmsnorm_gate_mm" not in hip_calls and "ws_residual_mm" not in hip_calls
+        expected.backward()
+        hip_calls.clear()
+        result.backward()
+        for name in ("ws_linear_ce_fused_backward", "ws_swiglu_backward_mm", "ws_mm_store_f32",
+                     "ws_mm_store_f32_group", "ws_rmsnorm_backward"):
+            assert name in hip_calls, (name, hip_calls)
+        assert not any(call.startswith("ws_mm_accumulate") for call in hip_calls), hip_calls
+        assert math.isclose(result.item(), expected.item(), rel_tol=1e-3)
+        for (name, p), q in zip(reference.named_parameters(), actual.parameters(), strict=True):
+            assert q.grad is not None and q.grad.dtype == torch.float32, name
+            cos = torch.nn.functional.cosine_similarity(q.grad.flatten().double(),
+                                                        p.grad.flatten().double(), dim=0).item()
+            assert cos > 0.999 and _rel(q.grad, p.grad) < 0.02, (name, cos, _rel(q.grad, p.grad))
+        assert tuple(actual.state_dict()) == keys
+        actual.eval()
+        with torch.no_grad():
+            hip_calls.clear()
+            assert actual(inputs).shape == (*tokens, vocab)
+            assert not hip_calls
+    finally:
+        torch._dynamo.reset()
 
 
 def test_fused_adapter_refuses_second_application_and_bf16_masters():

@@ -326,6 +326,48 @@ def test_grouped_accumulation_falls_back_to_single_launches(case):
         assert_f32_close(gg.cpu(), oracle.accumulate_weight_grad(g, a, b), f"{case} gradient {i}")
 
 
+@pytest.mark.parametrize("round_bf16", [True, False])
+@pytest.mark.parametrize("case", ["whole_tiles", "balanced", "even_slices", "generic"])
+def test_fp32_store_equals_accumulation_into_zeros_bitwise(case, round_bf16):
+    """ws_mm_store_f32 writes G = f32(r(A @ B)) without reading G: on every path (whole
+    tiles, balanced stream-K, even split-K slices, the generic loader) it equals
+    accumulation into a zeroed buffer bit for bit, whatever G held before (here NaN)."""
+    from ops.fused_execution import mm_accumulate_, mm_f32
+
+    shapes = {"whole_tiles": (1024, 16 * 256, 16 * 256, 1),
+              "balanced": (1000, 17 * 256 - 96, 16 * 256 - 40, 2),
+              "even_slices": (3000, 304, 264, 2),
+              "generic": (700, 300, 262, 2)}
+    tokens, n_out, n_in, splits = shapes[case]
+    gen = _gen(91)
+    dy = torch.randn(tokens, n_out, generator=gen).bfloat16().cuda()
+    x = torch.randn(tokens, n_in, generator=gen).bfloat16().cuda()
+    want = torch.zeros(n_out, n_in, device="cuda")
+    mm_accumulate_(want, dy.T, x, round_bf16, splits)
+    got = torch.full((n_out, n_in), float("nan"), device="cuda")
+    mm_accumulate_(got, dy.T, x, round_bf16, splits, _entry="ws_mm_store_f32")
+    fresh = mm_f32(dy.T, x, round_bf16, splits=splits)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want) and torch.equal(fresh, want)
+    rows = torch.arange(0, n_out, 37)
+    assert_f32_close(got.cpu()[rows], oracle.accumulate_weight_grad(
+        torch.zeros(len(rows), n_in), dy.cpu().T[rows], x.cpu(), round_bf16), f"store {case}")
+
+
+def test_grouped_fp32_store_equals_grouped_accumulation_into_zeros_bitwise():
+    """ws_mm_store_f32_group on the MLP's two weight gradients (one launch, shared tiles)
+    equals the grouped accumulation into zeroed buffers bit for bit."""
+    from ops.fused_execution import mm_accumulate_group_, mm_f32_group
+
+    cases = _group_case(86, 520, [(2000, 4000), (4000, 2104), (296, 296)])
+    zeros = [torch.zeros_like(gg) for _, _, _, gg, _, _ in cases]
+    mm_accumulate_group_([(z, ga, gb) for z, (_, _, _, _, ga, gb) in zip(zeros, cases)], True)
+    got = mm_f32_group([(ga, gb) for _, _, _, _, ga, gb in cases])
+    torch.cuda.synchronize()
+    for i, (z, out) in enumerate(zip(zeros, got)):
+        assert torch.equal(z, out), i
+
+
 def test_weight_gradient_zero_upstream_leaves_buffer_bitwise():
     from ops.fused_execution import mm_accumulate_
 

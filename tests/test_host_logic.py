@@ -357,6 +357,43 @@ def test_fused_adapter_keeps_cpu_and_eval_paths_and_state():
         apply_fused_execution(_small_lm().bfloat16())
 
 
+def test_fused_adapter_on_the_inline_layout_keeps_cpu_paths_and_state():
+    """A model in the reference's own core layout (no seams) takes the module-level
+    attachment; on the CPU every patched module and the wrapped forward run the original
+    code: same loss and gradients bit for bit, same parameters and state dict."""
+    from inline_layout_model import InlineLM
+    from warpstate.config import WarpStateConfig
+
+    from ops.fused_training import apply_fused_execution
+
+    torch.manual_seed(574)
+    reference = InlineLM(WarpStateConfig(vocab_size=32, d_model=16, n_heads=2, n_cores=1,
+                                         logical_depth=2, ffn_hidden=24,
+                                         gradient_checkpointing=False,
+                                         loss_chunk_size=3)).train()
+    adapted = copy.deepcopy(reference)
+    keys, params = tuple(adapted.state_dict()), tuple(adapted.parameters())
+    apply_fused_execution(adapted)
+    assert tuple(adapted.state_dict()) == keys
+    assert all(a is b for a, b in zip(params, adapted.parameters(), strict=True))
+    # The module-level routes were installed (the core has no project / mix seams).
+    core = adapted.cores[0]
+    for module in (core.norm1, core.in_proj, core.out_proj, core.norm2, core.ffn, adapted.final_norm):
+        assert "forward" in vars(module), module
+    tokens = torch.randint(32, (2, 8))
+    labels = torch.randint(32, (2, 8))
+    labels.view(-1)[3:9] = -100
+    with torch.autocast("cpu", dtype=torch.bfloat16):
+        _, want = reference(tokens, labels, return_logits=False)
+        _, got = adapted(tokens, labels, return_logits=False)
+    assert torch.equal(got, want)
+    want.backward()
+    got.backward()
+    for p, q in zip(reference.parameters(), adapted.parameters(), strict=True):
+        assert torch.equal(p.grad, q.grad)
+    assert torch.equal(adapted(tokens), reference(tokens))
+
+
 def test_bf16_residuals_make_the_stream_bf16_only_under_autocast():
     from ops.residual_experiment import apply_bf16_residuals
 

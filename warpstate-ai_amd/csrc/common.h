@@ -20,6 +20,10 @@ typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
 namespace ws {
 
 constexpr int kWave = 64;
+// FP32 accumulation mode bits (GemmParams::round_acc and the split-K reductions):
+// kAccRound rounds each product to BF16 before it is added, kAccStore stores f32(.) into
+// G instead of adding it (G is not read).
+enum AccMode { kAccRound = 1, kAccStore = 2 };
 // Byte offset that is always beyond a buffer resource's num_records: loads through it
 // return zero and stores through it are dropped by the buffer unit.
 constexpr unsigned kOOB = 0x80000000u;

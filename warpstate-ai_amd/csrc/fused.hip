@@ -175,7 +175,7 @@ struct SkOutputs {
   GemmMember m[kMaxGroup];
 };
 
-// G[m, n] += f32(r(sum of the tile's pieces)) for the stream-K tiles of a balanced
+// G[m, n] += f32(r(sum of the tile's pieces)) (= with kAccStore) for the stream-K tiles of a balanced
 // accumulation: block (tile ti, chunk) handles 1024 elements of tile ti's 256 x 256 block,
 // four consecutive columns per thread; pieces are added in k order. Tile ti is launch
 // raster index dp_tiles + ti, in the output of the member whose tiles hold it.
@@ -202,15 +202,16 @@ __global__ void __launch_bounds__(256) sk_accum_kernel(const float* __restrict__
   const float* src = ws + ti * pieces_max * (long)(kFBM * kFBN) + e;
   f32x4_t s = *reinterpret_cast<const f32x4_t*>(src);
   for (int q = 1; q < pieces; ++q) s += *reinterpret_cast<const f32x4_t*>(src + (long)q * kFBM * kFBN);
-  if (round_acc) {
+  if (round_acc & kAccRound) {
 #pragma unroll
     for (int d = 0; d < 4; ++d) s[d] = rbf16(s[d]);
   }
   float* dst = g + (long)m * ldg + n;
+  const bool store = round_acc & kAccStore;
   if (vec && n + 3 < N) {
-    *reinterpret_cast<f32x4_t*>(dst) = *reinterpret_cast<const f32x4_t*>(dst) + s;
+    *reinterpret_cast<f32x4_t*>(dst) = store ? s : *reinterpret_cast<const f32x4_t*>(dst) + s;
   } else {
-    for (int d = 0; d < 4 && n + d < N; ++d) dst[d] += s[d];
+    for (int d = 0; d < 4 && n + d < N; ++d) dst[d] = store ? s[d] : dst[d] + s[d];
   }
 }
 
@@ -224,10 +225,13 @@ extern "C" int64_t ws_mm_accumulate_workspace_floats(int64_t m, int64_t n, int64
   return even > balanced ? even : balanced;
 }
 
-extern "C" int ws_mm_accumulate_f32(const void* a, int64_t a_s0, int64_t a_s1, const void* b,
-                                    int64_t b_s0, int64_t b_s1, float* g, int64_t ldg, int64_t m,
-                                    int64_t n, int64_t k, int round_bf16, float* workspace,
-                                    int64_t splits, void* stream) {
+namespace {
+
+// G = or += f32(r(A B)) (`acc`: AccMode bits) through the tile, balanced stream-K or even
+// split-K paths; the body of ws_mm_accumulate_f32 and ws_mm_store_f32.
+int mm_f32(const void* a, int64_t a_s0, int64_t a_s1, const void* b, int64_t b_s0, int64_t b_s1,
+           float* g, int64_t ldg, int64_t m, int64_t n, int64_t k, int acc, float* workspace,
+           int64_t splits, void* stream) {
   if (int rc = check_gemm_args(a, a_s0, a_s1, b, b_s0, b_s1, g, m, n, k)) return rc;
   if (ldg < n) return set_error(kInvalid, "gradient leading dimension %ld < n", (long)ldg);
   if (splits < 1 || splits > 64) return set_error(kInvalid, "splits must be in [1, 64]");
@@ -238,7 +242,7 @@ extern "C" int ws_mm_accumulate_f32(const void* a, int64_t a_s0, int64_t a_s1, c
   p.a = desc_a(a, a_s0, a_s1);
   p.b = desc_b(b, b_s0, b_s1);
   p.M = (int)m; p.N = (int)n; p.K = (int)k;
-  p.round_acc = round_bf16 ? 1 : 0;
+  p.round_acc = acc;
   int am = operand_mode(p.a, m, k, 256), bm = operand_mode(p.b, n, k, 256);
   p.g = g;
   p.ldg = ldg;
@@ -270,7 +274,7 @@ extern "C" int ws_mm_accumulate_f32(const void* a, int64_t a_s0, int64_t a_s1, c
     out.m[0] = GemmMember{p.a, p.b, (int)m, (int)n, plan.tiles_m, plan.tiles_n, 0, g, (long)ldg};
     hipLaunchKernelGGL(sk_accum_kernel, dim3((unsigned)(plan.sk_tiles * 64)), dim3(256), 0, s,
                        workspace, out, plan.dp_tiles, plan.k_tiles, plan.units, plan.sk_workers,
-                       plan.pieces, round_bf16 ? 1 : 0, p.vec_out);
+                       plan.pieces, acc, p.vec_out);
     return hip_check(hipGetLastError(), "stream-K reduce launch");
   }
   // Fewer tiles than compute units, or generic layouts: even split-K slices through the
@@ -290,8 +294,26 @@ extern "C" int ws_mm_accumulate_f32(const void* a, int64_t a_s0, int64_t a_s1, c
   const long threads = vec ? m * n / 4 : m * n;
   hipLaunchKernelGGL(splitk_accum_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s,
                      workspace, (int)splits, (long)(m * n), g, (long)ldg, (int)m, (int)n,
-                     round_bf16 ? 1 : 0, vec);
+                     acc, vec);
   return hip_check(hipGetLastError(), "split-K reduce launch");
+}
+
+}  // namespace
+
+extern "C" int ws_mm_accumulate_f32(const void* a, int64_t a_s0, int64_t a_s1, const void* b,
+                                    int64_t b_s0, int64_t b_s1, float* g, int64_t ldg, int64_t m,
+                                    int64_t n, int64_t k, int round_bf16, float* workspace,
+                                    int64_t splits, void* stream) {
+  return mm_f32(a, a_s0, a_s1, b, b_s0, b_s1, g, ldg, m, n, k, round_bf16 ? kAccRound : 0,
+                workspace, splits, stream);
+}
+
+extern "C" int ws_mm_store_f32(const void* a, int64_t a_s0, int64_t a_s1, const void* b,
+                               int64_t b_s0, int64_t b_s1, float* g, int64_t ldg, int64_t m,
+                               int64_t n, int64_t k, int round_bf16, float* workspace,
+                               int64_t splits, void* stream) {
+  return mm_f32(a, a_s0, a_s1, b, b_s0, b_s1, g, ldg, m, n, k,
+                kAccStore | (round_bf16 ? kAccRound : 0), workspace, splits, stream);
 }
 
 namespace {
@@ -340,9 +362,10 @@ extern "C" int64_t ws_mm_accumulate_group_workspace_floats(const ws_accumulate_p
   return need;
 }
 
-extern "C" int ws_mm_accumulate_f32_group(const ws_accumulate_problem* problems, int count,
-                                          int64_t k, int round_bf16, float* workspace,
-                                          void* stream) {
+namespace {
+
+int mm_f32_group(const ws_accumulate_problem* problems, int count, int64_t k, int acc,
+                 float* workspace, void* stream) {
   if (!problems) return set_error(kInvalid, "null problem table");
   if (count < 1 || count > kMaxGroup)
     return set_error(kInvalid, "group size %d outside [1, %d]", count, kMaxGroup);
@@ -371,7 +394,7 @@ extern "C" int ws_mm_accumulate_f32_group(const ws_accumulate_problem* problems,
   // vector outputs, and the tiles fill at least one round.
   GemmParams p{};
   p.K = (int)k;
-  p.round_acc = round_bf16 ? 1 : 0;
+  p.round_acc = acc;
   p.vec_out = 1;
   int am = -1, bm = -1;
   bool one_launch = plan.dp_tiles > 0 && (plan.sk_tiles == 0 || (workspace && al(workspace, 16)));
@@ -399,8 +422,8 @@ extern "C" int ws_mm_accumulate_f32_group(const ws_accumulate_problem* problems,
     for (int i = 0; i < count; ++i) {
       const ws_accumulate_problem& q = problems[i];
       const int splits = workspace ? auto_splits(q.m, q.n, k, workers) : 1;
-      if (int rc = ws_mm_accumulate_f32(q.a, q.a_s0, q.a_s1, q.b, q.b_s0, q.b_s1, q.g, q.ldg, q.m,
-                                        q.n, k, round_bf16, workspace, splits, stream))
+      if (int rc = mm_f32(q.a, q.a_s0, q.a_s1, q.b, q.b_s0, q.b_s1, q.g, q.ldg, q.m, q.n, k, acc,
+                          workspace, splits, stream))
         return rc;
     }
     return kOk;
@@ -425,6 +448,20 @@ extern "C" int ws_mm_accumulate_f32_group(const ws_accumulate_problem* problems,
   for (int i = 0; i < count; ++i) out.m[i] = p.grp[i];
   hipLaunchKernelGGL(sk_accum_kernel, dim3((unsigned)(plan.sk_tiles * 64)), dim3(256), 0, s,
                      workspace, out, plan.dp_tiles, plan.k_tiles, plan.units, plan.sk_workers,
-                     plan.pieces, round_bf16 ? 1 : 0, 1);
+                     plan.pieces, acc, 1);
   return hip_check(hipGetLastError(), "stream-K reduce launch");
+}
+
+}  // namespace
+
+extern "C" int ws_mm_accumulate_f32_group(const ws_accumulate_problem* problems, int count,
+                                          int64_t k, int round_bf16, float* workspace,
+                                          void* stream) {
+  return mm_f32_group(problems, count, k, round_bf16 ? kAccRound : 0, workspace, stream);
+}
+
+extern "C" int ws_mm_store_f32_group(const ws_accumulate_problem* problems, int count, int64_t k,
+                                     int round_bf16, float* workspace, void* stream) {
+  return mm_f32_group(problems, count, k, kAccStore | (round_bf16 ? kAccRound : 0), workspace,
+                      stream);
 }

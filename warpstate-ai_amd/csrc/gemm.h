@@ -73,7 +73,7 @@ struct GemmParams {
   float* g; long ldg; long split_stride;
   int gate_lo, gate_hi;
   int eager;
-  int round_acc;
+  int round_acc;  // AccMode bits (common.h)
   const long* targets;
   const float* lse;
   float* part_max; float* part_sum; float* tgt_logit; int parts_per_row;
@@ -549,9 +549,9 @@ struct EpiAccF32 {
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
               float x = acc.v[i][j][4 * g + e];
-              add[e] = (!SPLIT && p.round_acc) ? rbf16(x) : x;
+              add[e] = (!SPLIT && (p.round_acc & kAccRound)) ? rbf16(x) : x;
             }
-            if (!SPLIT) {
+            if (!SPLIT && !(p.round_acc & kAccStore)) {
               f32x4_t old = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rg, off, 0, 0));
               add = old + add;
             }
@@ -563,7 +563,10 @@ struct EpiAccF32 {
                 float x = acc.v[i][j][4 * g + e];
                 float* dst = gbase + (long)(m - m0) * p.ldg + (n + e - n0);
                 if (SPLIT) *dst = x;
-                else *dst += p.round_acc ? rbf16(x) : x;
+                else {
+                  const float v = (p.round_acc & kAccRound) ? rbf16(x) : x;
+                  *dst = (p.round_acc & kAccStore) ? v : *dst + v;
+                }
               }
             }
           }

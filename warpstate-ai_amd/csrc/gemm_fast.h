@@ -492,7 +492,8 @@ struct FEpiSwigluBwd {
   }
 };
 
-// FP32 accumulation (EpiAccF32 numerics); raw FP32 split-K partials when SPLIT.
+// FP32 accumulation (EpiAccF32 numerics); raw FP32 split-K partials when SPLIT. With
+// kAccStore in round_acc the tile is stored instead (G = f32(r(A B)), G not read).
 template <bool SPLIT>
 struct FEpiAccF32 {
   template <int FA, int FB>
@@ -524,9 +525,9 @@ struct FEpiAccF32 {
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const float x = acc.v[i][j][e];
-            add[e] = (!SPLIT && round_acc) ? rbf16(x) : x;
+            add[e] = (!SPLIT && (round_acc & kAccRound)) ? rbf16(x) : x;
           }
-          if (!SPLIT) {
+          if (!SPLIT && !(round_acc & kAccStore)) {
             f32x4_t old = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rg, off, 0, 0));
             add = old + add;
           }

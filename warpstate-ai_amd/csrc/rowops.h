@@ -547,7 +547,7 @@ static __global__ void ce_scale_kernel(const float* __restrict__ dmean, const lo
 
 // ---------------------------------------------------------------------------------------
 // Split-K reductions. Partials are [splits][M][N] FP32 slices of one GEMM output.
-// G[m, n] += f32(r(sum_s P_s)) (round) or G += sum_s P_s. With `vec` (N and ldg multiples of
+// G[m, n] += f32(r(sum_s P_s)) (round) or G += sum_s P_s; with kAccStore, G = (the same). With `vec` (N and ldg multiples of
 // 4, 16-byte aligned buffers) each thread moves four columns with 16-byte accesses.
 static __global__ void __launch_bounds__(256) splitk_accum_kernel(const float* __restrict__ part,
                                                            int splits, long split_stride,
@@ -560,12 +560,12 @@ static __global__ void __launch_bounds__(256) splitk_accum_kernel(const float* _
     const long e = 4 * i, m = e / N, n = e % N;
     f32x4_t s = *reinterpret_cast<const f32x4_t*>(part + e);
     for (int q = 1; q < splits; ++q) s += *reinterpret_cast<const f32x4_t*>(part + q * split_stride + e);
-    if (round_acc) {
+    if (round_acc & kAccRound) {
 #pragma unroll
       for (int d = 0; d < 4; ++d) s[d] = rbf16(s[d]);
     }
     f32x4_t* dst = reinterpret_cast<f32x4_t*>(g + m * ldg + n);
-    *dst = *dst + s;
+    *dst = (round_acc & kAccStore) ? s : *dst + s;
     return;
   }
   const long total = (long)M * N;
@@ -573,7 +573,8 @@ static __global__ void __launch_bounds__(256) splitk_accum_kernel(const float* _
   const long m = i / N, n = i % N;
   float s = 0.0f;
   for (int q = 0; q < splits; ++q) s += part[q * split_stride + m * N + n];
-  g[m * ldg + n] += round_acc ? rbf16(s) : s;
+  const float v = (round_acc & kAccRound) ? rbf16(s) : s;
+  g[m * ldg + n] = (round_acc & kAccStore) ? v : g[m * ldg + n] + v;
 }
 
 // out[m, n] = r(sum_s P_s) as BF16.

@@ -54,6 +54,9 @@ SIGNATURES = {
                                     _i64, _i64, _i64, _i32, _c_void_p, _i64, _c_void_p]),
     "ws_mm_accumulate_group_workspace_floats": (_i64, [_c_void_p, _i32, _i64]),
     "ws_mm_accumulate_f32_group": (_i32, [_c_void_p, _i32, _i64, _i32, _c_void_p, _c_void_p]),
+    "ws_mm_store_f32": (_i32, [_c_void_p, _i64, _i64, _c_void_p, _i64, _i64, _c_void_p, _i64,
+                               _i64, _i64, _i64, _i32, _c_void_p, _i64, _c_void_p]),
+    "ws_mm_store_f32_group": (_i32, [_c_void_p, _i32, _i64, _i32, _c_void_p, _c_void_p]),
     "ws_linear_ce_parts": (_i64, [_i64]),
     "ws_linear_ce_forward": (_i32, [_c_void_p, _i64, _c_void_p, _i64, _c_void_p, _i64, _i64, _i64,
                                     _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,

@@ -254,7 +254,8 @@ def auto_splits(m: int, n: int, k: int, cus: int = 256, tile: int = 256,
 
 
 def mm_accumulate_(g: torch.Tensor, a: torch.Tensor, b: torch.Tensor, round_bf16: bool = True,
-                   splits: int | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
+                   splits: int | None = None, workspace: torch.Tensor | None = None,
+                   _entry: str = "ws_mm_accumulate_f32") -> torch.Tensor:
     """G += f32(r(a @ b)) (or G += a @ b in FP32 when ``round_bf16`` is False), in place.
 
     G is FP32 [M, N] with unit column stride. ``splits`` > 1 lets the reduction be split
@@ -273,14 +274,27 @@ def mm_accumulate_(g: torch.Tensor, a: torch.Tensor, b: torch.Tensor, round_bf16
     need = _hip.query("ws_mm_accumulate_workspace_floats", m, n, k, splits)
     if need and (workspace is None or workspace.numel() < need):
         workspace = torch.empty((need,), dtype=torch.float32, device=g.device)
-    _hip.call("ws_mm_accumulate_f32", a.data_ptr(), a.stride(0), a.stride(1), b.data_ptr(),
+    _hip.call(_entry, a.data_ptr(), a.stride(0), a.stride(1), b.data_ptr(),
               b.stride(0), b.stride(1), g.data_ptr(), g.stride(0), m, n, k, int(round_bf16),
               None if not need else workspace.data_ptr(), splits, _hip.stream(a))
     return g
 
 
+def mm_f32(a: torch.Tensor, b: torch.Tensor, round_bf16: bool = True,
+           out: torch.Tensor | None = None, splits: int | None = None) -> torch.Tensor:
+    """f32(r(a @ b)) as a new FP32 [M, N] tensor (``out`` when given), written in one pass
+    by the FP32 GEMM epilogue without reading or clearing the buffer
+    (``ws_mm_store_f32``): the BF16 weight gradient of F.linear widened to FP32.
+    ``splits`` as in ``mm_accumulate_``."""
+    m, n = a.shape[0], b.shape[1]
+    if out is None:
+        out = torch.empty((m, n), dtype=torch.float32, device=a.device)
+    return mm_accumulate_(out, a, b, round_bf16, splits, _entry="ws_mm_store_f32")
+
+
 def mm_accumulate_group_(items, round_bf16: bool = True,
-                         workspace: torch.Tensor | None = None) -> None:
+                         workspace: torch.Tensor | None = None,
+                         _entry: str = "ws_mm_accumulate_f32_group") -> None:
     """G_i += f32(r(a_i @ b_i)) for up to four (G_i, a_i, b_i) with the same reduction
     length, in place and in one launch (``ws_mm_accumulate_f32_group``): the tiles of all
     gradients share the GPU, so a gradient with fewer 256 x 256 tiles than compute units
@@ -308,8 +322,19 @@ def mm_accumulate_group_(items, round_bf16: bool = True,
     need = _hip.query("ws_mm_accumulate_group_workspace_floats", table, len(rows), k)
     if need and (workspace is None or workspace.numel() < need):
         workspace = torch.empty((need,), dtype=torch.float32, device=first.device)
-    _hip.call("ws_mm_accumulate_f32_group", table, len(rows), k, int(round_bf16),
+    _hip.call(_entry, table, len(rows), k, int(round_bf16),
               None if not need else workspace.data_ptr(), _hip.stream(items[0][1]))
+
+
+def mm_f32_group(pairs, round_bf16: bool = True) -> list[torch.Tensor]:
+    """[f32(r(a_i @ b_i))] for up to four (a_i, b_i) with the same reduction length, as new
+    FP32 tensors written in one launch without clearing (``ws_mm_store_f32_group``): the
+    weight gradients of one backward stage sharing the GPU's tiles."""
+    outs = [torch.empty((a.shape[0], b.shape[1]), dtype=torch.float32, device=a.device)
+            for a, b in pairs]
+    mm_accumulate_group_([(g, a, b) for g, (a, b) in zip(outs, pairs)], round_bf16,
+                         _entry="ws_mm_store_f32_group")
+    return outs
 
 
 class CrossEntropyState:

@@ -1,34 +1,46 @@
 """Route a WarpState model's training step through the fused HIP GEMMs (additive adapter).
 
-``apply_fused_execution(model)`` replaces, for eligible training calls, the parts of each
-core and of the loss that the fused kernels of ``ops.fused_execution`` cover:
+``apply_fused_execution(model)`` attaches each core at the finest boundary it offers.
+
+A core that exposes the ``project`` / ``mix`` seams runs as a whole through three fused
+operators, for eligible training calls:
 
 * ``project``: norm1 -> in_proj -> sigmoid on the gate slice (warpstate/model.py:107-112,
   :120-121, :174) becomes one ``rmsnorm_gate_mm`` (RMSNorm row pass, projection with the
   sigmoid in its epilogue);
 * the attention output projection with its residual add (warpstate/model.py:177) and
   the SwiGLU block with its residual add (warpstate/model.py:52-60, :178) become
-  ``residual_mm`` and ``launch_swiglu_mm`` + ``residual_mm``;
-* the chunked tied-head loss (warpstate/model.py:316-334) becomes the fused
-  cross-entropy (``linear_cross_entropy``), which never holds the full [rows, vocab]
-  logits in HBM (one row chunk's BF16 logits at a time in its one-pass mode).
+  ``residual_mm`` and ``launch_swiglu_mm`` + ``residual_mm``.
 
-Each core piece is a registered operator (``warpstate::fused_norm_projection``,
-``warpstate::fused_residual_projection``, ``warpstate::fused_swiglu_block``) with a fake
-implementation and an autograd formula whose backward is another operator, so the patched
-core compiles with ``torch.compile(fullgraph=True)`` as the reference compiles its cores
+A core in the reference's own layout (``WarpStateCore.forward`` as one method,
+warpstate/model.py:114-178: ``_split`` around in_proj, the gate sigmoid and both residual
+adds inline) is attached module by module: its RMSNorm modules go to the RMSNorm row
+kernel, its bias-free Linear modules to this library's GEMM, and its SwiGLU module to the
+paired projection with the SwiGLU epilogue plus the down GEMM. What needs the seams (the
+gate sigmoid in the projection's epilogue, the residual adds in the projections'
+epilogues) stays in the core's own code.
+
+The tied-head loss (warpstate/model.py:316-334) becomes the fused cross-entropy
+(``linear_cross_entropy``), which never holds the full [rows, vocab] logits in HBM (one
+row chunk's BF16 logits at a time in its one-pass mode): through a ``chunked_loss`` seam,
+or else by wrapping the model's forward in the style of ops/loss_experiment.py:44-52.
+
+Every piece is a registered operator with a fake implementation and an autograd formula
+whose backward is another operator, so patched cores compile with
+``torch.compile(fullgraph=True)`` as the reference compiles its cores
 (run_40b.py:430-438). The backward operators are built from the fused backward kernels
 (the gate-sigmoid backward, the SwiGLU backward fused on the dAct GEMM, the RMSNorm
 backward) and ``dgrad_mm`` for the input gradients. A projection weight's gradient is
-f32(r(dY^T X)) from the FP32-accumulating GEMM (the MLP's two in one grouped launch),
-returned through autograd like the reference's BF16 dW (test_gradient_execution.py:243-246):
+f32(r(dY^T X)), the reference's BF16 weight gradient widened to FP32
+(test_gradient_execution.py:243-246), written by the FP32 GEMM epilogue in one pass into a
+fresh buffer (the MLP's two in one grouped launch) and returned through autograd:
 autograd's accumulation into the FP32 master's ``.grad``, and any gradient hook (DDP's),
 see it as usual.
 
-A core call is eligible in training mode with gradients on, under BF16 autocast, on a BF16
-CUDA residual stream (``ops.residual_experiment.apply_bf16_residuals``) and bias-free
-projections; everything else runs the original forwards. The token mixer between the
-projections (``core.mix``) is the model's own code.
+A call is eligible in training mode with gradients on, under BF16 autocast, on CUDA; the
+core operators and the RMSNorm modules also need a BF16 residual stream
+(``ops.residual_experiment.apply_bf16_residuals``), and projections must be bias-free.
+Everything else runs the original forwards.
 """
 
 from __future__ import annotations
@@ -76,8 +88,7 @@ def fused_norm_projection_backward(dout: Tensor, x: Tensor, norm_weight: Tensor,
 
     dp = fx.sigmoid_backward_cols(dout.contiguous(), out, (gate_begin, gate_end))
     dy = fx.dgrad_mm(dp, w)
-    dw = torch.zeros(w.shape, dtype=F32, device=w.device)
-    fx.mm_accumulate_(dw, dp.T, normed, True)
+    dw = fx.mm_f32(dp.T, normed)
     dx, dnorm = _rms_backward(x, norm_weight, rstd, dy, True)
     return dx, dnorm, dw
 
@@ -128,9 +139,7 @@ def fused_residual_projection_backward(dout: Tensor, a: Tensor, w: Tensor
                                        ) -> tuple[Tensor, Tensor]:
     """(dA, dW): dA = r(dOut @ W), dW = f32(r(dOut^T A))."""
     dout = dout.contiguous()
-    dw = torch.zeros(w.shape, dtype=F32, device=w.device)
-    fx.mm_accumulate_(dw, dout.T, a, True)
-    return fx.dgrad_mm(dout, w), dw
+    return fx.dgrad_mm(dout, w), fx.mm_f32(dout.T, a)
 
 
 @fused_residual_projection_backward.register_fake
@@ -186,9 +195,7 @@ def fused_swiglu_block_backward(dout: Tensor, h: Tensor, packed: Tensor, act: Te
     dh = r(dPacked @ W_upgate)."""
     dout = dout.contiguous()
     dpacked = fx.swiglu_backward_mm(dout, wd, packed, True)
-    g_upgate = torch.zeros(wug.shape, dtype=F32, device=wug.device)
-    g_down = torch.zeros(wd.shape, dtype=F32, device=wd.device)
-    fx.mm_accumulate_group_([(g_down, dout.T, act), (g_upgate, dpacked.T, h)], True)
+    g_down, g_upgate = fx.mm_f32_group([(dout.T, act), (dpacked.T, h)])
     return fx.dgrad_mm(dpacked, wug), g_upgate, g_down
 
 
@@ -210,6 +217,113 @@ def _swiglu_block_autograd(ctx, dout, _dpacked, _dact, _dwug, _dwd):
 
 
 fused_swiglu_block.register_autograd(_swiglu_block_autograd, setup_context=_swiglu_block_setup)
+
+
+# --- module-level pieces (models whose cores expose no seams) --------------------------------
+
+@custom_op("warpstate::fused_linear", mutates_args=())
+def fused_linear(a: Tensor, weight: Tensor) -> tuple[Tensor, Tensor]:
+    """(r(A @ W^T), W_bf16) for rows A [rows, k] BF16 and the FP32 master W [n, k]: a
+    bias-free nn.Linear under BF16 autocast on this library's GEMM."""
+    w = weight.to(BF16)
+    return fx.mm(a, w.T), w
+
+
+@fused_linear.register_fake
+def _linear_fake(a, weight):
+    return a.new_empty((a.shape[0], weight.shape[0])), weight.new_empty(weight.shape, dtype=BF16)
+
+
+@custom_op("warpstate::fused_linear_backward", mutates_args=())
+def fused_linear_backward(dout: Tensor, a: Tensor, w: Tensor) -> tuple[Tensor, Tensor]:
+    """(dA, dW): dA = r(dOut @ W), dW = f32(r(dOut^T A)) written in one FP32 pass."""
+    dout = dout.contiguous()
+    return fx.dgrad_mm(dout, w), fx.mm_f32(dout.T, a)
+
+
+@fused_linear_backward.register_fake
+def _linear_backward_fake(dout, a, w):
+    return torch.empty_like(a), w.new_empty(w.shape, dtype=F32)
+
+
+def _linear_setup(ctx, inputs, output):
+    ctx.save_for_backward(inputs[0], output[1])
+
+
+def _linear_autograd(ctx, dout, _dw):
+    a, w = ctx.saved_tensors
+    return fused_linear_backward(dout, a, w)
+
+
+fused_linear.register_autograd(_linear_autograd, setup_context=_linear_setup)
+
+
+@custom_op("warpstate::fused_swiglu_mlp", mutates_args=())
+def fused_swiglu_mlp(h: Tensor, w_upgate: Tensor, w_down: Tensor
+                     ) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """(down(silu(gate) * up), packed, act, W_upgate_bf16, W_down_bf16): the SwiGLU module
+    (warpstate/model.py:52-60) as the paired projection with the SwiGLU epilogue and the
+    down projection, eager BF16 rounding; the caller keeps its own residual add."""
+    from ops.matmul_epilogue import launch_swiglu_mm
+
+    wug, wd = w_upgate.to(BF16), w_down.to(BF16)
+    packed, act = launch_swiglu_mm(h, wug.T, "persistent", (128, 128, 32, 8, 3), True)
+    return fx.mm(act, wd.T), packed, act, wug, wd
+
+
+@fused_swiglu_mlp.register_fake
+def _swiglu_mlp_fake(h, w_upgate, w_down):
+    rows, two_h = h.shape[0], w_upgate.shape[0]
+    return (h.new_empty((rows, w_down.shape[0])), h.new_empty((rows, two_h)),
+            h.new_empty((rows, two_h // 2)), w_upgate.new_empty(w_upgate.shape, dtype=BF16),
+            w_down.new_empty(w_down.shape, dtype=BF16))
+
+
+def _swiglu_mlp_setup(ctx, inputs, output):
+    _out, packed, act, wug, wd = output
+    ctx.save_for_backward(inputs[0], packed, act, wug, wd)
+
+
+def _swiglu_mlp_autograd(ctx, dout, _dpacked, _dact, _dwug, _dwd):
+    h, packed, act, wug, wd = ctx.saved_tensors
+    return fused_swiglu_block_backward(dout, h, packed, act, wug, wd)
+
+
+fused_swiglu_mlp.register_autograd(_swiglu_mlp_autograd, setup_context=_swiglu_mlp_setup)
+
+
+def _rows_bf16(x: Tensor) -> Tensor:
+    return x.reshape(-1, x.shape[-1]).to(BF16).contiguous()
+
+
+def _linear_forward(module, x, original):
+    if module.bias is not None:
+        return original(x)
+    out = fused_linear(_rows_bf16(x), module.weight)[0]
+    return out.view(*x.shape[:-1], module.out_features)
+
+
+def _swiglu_forward(module, x, original):
+    if module.up_gate.bias is not None or module.down.bias is not None:
+        return original(x)
+    out = fused_swiglu_mlp(_rows_bf16(x), module.up_gate.weight, module.down.weight)[0]
+    return out.view(*x.shape[:-1], module.down.out_features)
+
+
+def _rms_forward(module, x, original):
+    from ops.activation_execution import bf16_rmsnorm
+
+    if not (x.dtype == BF16 and x.is_contiguous() and 0 < x.shape[-1] <= 8192):
+        return original(x)  # an FP32 residual stream keeps the original FP32 arithmetic
+    return bf16_rmsnorm(x, module.weight, float(module.eps), True)[0]
+
+
+class _HiddenReady(Exception):
+    """Carries the final norm's output out of the model's own forward."""
+
+    def __init__(self, hidden):
+        super().__init__()
+        self.hidden = hidden
 
 
 # --- the adapter ---------------------------------------------------------------------------
@@ -237,30 +351,111 @@ def _fused_core_forward(core, x: torch.Tensor) -> torch.Tensor:
     return rows.view(x.shape)
 
 
+def _attach_modules(core) -> None:
+    """Module-level routing of a core without seams (the reference's WarpStateCore layout,
+    warpstate/model.py:114-178): its RMSNorm modules, bias-free Linear modules and SwiGLU
+    module, each for eligible calls only. The gate sigmoid and the residual adds stay inline
+    in the core's forward, so they are not fused."""
+    from warpstate.model import RMSNorm, SwiGLU
+
+    from ops._patching import install_forward
+
+    inside_swiglu = set()
+    for module in core.modules():
+        if isinstance(module, SwiGLU):
+            install_forward(module, _swiglu_forward)
+            inside_swiglu.update(id(m) for m in module.modules())
+    for module in core.modules():
+        if isinstance(module, RMSNorm):
+            install_forward(module, _rms_forward)
+        elif isinstance(module, torch.nn.Linear) and id(module) not in inside_swiglu:
+            install_forward(module, _linear_forward)
+
+
+def _attach_core(core) -> None:
+    """Core-level routing of a core that exposes the ``project`` / ``mix`` seams: the
+    RMSNorm-prologue projection with the gate sigmoid and both residual epilogues fused."""
+    original = core.forward
+
+    def core_forward(x, _core=core, _original=original):
+        if _core_eligible(_core, x):
+            return _fused_core_forward(_core, x)
+        return _original(x)
+
+    core.forward = core_forward
+
+
+def _loss_eligible(model, input_ids: Tensor) -> bool:
+    return (model.training and torch.is_grad_enabled() and input_ids.is_cuda
+            and torch.is_autocast_enabled("cuda")
+            and torch.get_autocast_dtype("cuda") == BF16)
+
+
+def _attach_loss(model) -> None:
+    """The tied-head loss through the fused cross-entropy. A model with a ``chunked_loss``
+    seam has it replaced; otherwise the model's forward is wrapped in the style of
+    ops/loss_experiment.py:44-52: a training call with targets and return_logits=False runs
+    the model's own forward up to ``final_norm`` (a forward hook takes its output and stops
+    the forward there, before the logits exist) and the fused loss on that hidden state."""
+    if hasattr(model, "chunked_loss"):
+        original_loss = model.chunked_loss
+
+        def chunked_loss(x, targets):
+            if not bf16_autocast_training(model, x):
+                return original_loss(x, targets)
+            mean, _per_token = fx.linear_cross_entropy(x.reshape(-1, x.shape[-1]),
+                                                       model.embed.weight, targets.reshape(-1))
+            return mean
+
+        model.chunked_loss = chunked_loss
+        return
+    original_forward = model.forward
+
+    def forward(input_ids, targets=None, *, return_logits=True):
+        if targets is None or return_logits or not _loss_eligible(model, input_ids):
+            return original_forward(input_ids, targets, return_logits=return_logits)
+
+        def stop(_module, _inputs, output):
+            raise _HiddenReady(output)
+
+        handle = model.final_norm.register_forward_hook(stop)
+        try:
+            original_forward(input_ids, None, return_logits=True)
+        except _HiddenReady as ready:
+            hidden = ready.hidden
+        else:
+            raise RuntimeError("the model's forward did not reach final_norm")
+        finally:
+            handle.remove()
+        mean, _per_token = fx.linear_cross_entropy(hidden.reshape(-1, hidden.shape[-1]),
+                                                   model.embed.weight, targets.reshape(-1))
+        return None, mean
+
+    model.forward = forward
+
+
 def apply_fused_execution(model: torch.nn.Module) -> None:
-    """Patch every core of ``model.cores`` and the model's ``chunked_loss``; apply once,
-    to a model with FP32 master parameters, before compiling or wrapping it."""
+    """Route ``model``'s cores and tied-head loss through the fused kernels; apply once, to
+    a model with FP32 master parameters, before compiling or wrapping it.
+
+    Each core is attached at the finest boundary it offers: a core with the ``project`` /
+    ``mix`` seams runs as a whole through the fused core operators; any other core (the
+    reference's layout) has its RMSNorm, Linear and SwiGLU modules routed one by one. The
+    loss replaces ``chunked_loss`` when the model has one, else wraps ``forward``."""
     if getattr(model, "_fused_execution", False):
         raise ValueError("Fused execution has already been applied")
     if any(p.dtype != torch.float32 for p in model.parameters()):
         raise ValueError("Fused execution requires FP32 master parameters")
-    for core in model.cores:
-        original = core.forward
+    seams = [callable(getattr(c, "mix", None)) and callable(getattr(c, "project", None))
+             for c in model.cores]
+    for core, has_seams in zip(model.cores, seams):
+        if has_seams:
+            _attach_core(core)
+        else:
+            _attach_modules(core)
+    if not all(seams):
+        from ops._patching import install_forward
 
-        def core_forward(x, _core=core, _original=original):
-            if _core_eligible(_core, x):
-                return _fused_core_forward(_core, x)
-            return _original(x)
-
-        core.forward = core_forward
-    original_loss = model.chunked_loss
-
-    def chunked_loss(x, targets):
-        if not bf16_autocast_training(model, x):
-            return original_loss(x, targets)
-        mean, _per_token = fx.linear_cross_entropy(x.reshape(-1, x.shape[-1]),
-                                                   model.embed.weight, targets.reshape(-1))
-        return mean
-
-    model.chunked_loss = chunked_loss
+        install_forward(model.final_norm, _rms_forward)
+    _attach_loss(model)
     model._fused_execution = True
