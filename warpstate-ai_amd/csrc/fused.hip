@@ -175,10 +175,11 @@ struct SkOutputs {
   GemmMember m[kMaxGroup];
 };
 
-// G[m, n] += f32(r(sum of the tile's pieces)) (= with kAccStore) for the stream-K tiles of a balanced
-// accumulation: block (tile ti, chunk) handles 1024 elements of tile ti's 256 x 256 block,
-// four consecutive columns per thread; pieces are added in k order. Tile ti is launch
-// raster index dp_tiles + ti, in the output of the member whose tiles hold it.
+// G[m, n] += f32(r(sum of the tile's pieces)) (=, G not read, with kAccStore) for the
+// stream-K tiles of a balanced accumulation: block (tile ti, chunk) handles 1024 elements
+// of tile ti's 256 x 256 block, four consecutive columns per thread; pieces are added in
+// k order. Tile ti is launch raster index dp_tiles + ti, in the output of the member whose
+// tiles hold it.
 __global__ void __launch_bounds__(256) sk_accum_kernel(const float* __restrict__ ws,
                                                        const SkOutputs out, int dp_tiles,
                                                        int k_tiles, long units, int workers,

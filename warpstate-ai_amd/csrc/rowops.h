@@ -547,8 +547,9 @@ static __global__ void ce_scale_kernel(const float* __restrict__ dmean, const lo
 
 // ---------------------------------------------------------------------------------------
 // Split-K reductions. Partials are [splits][M][N] FP32 slices of one GEMM output.
-// G[m, n] += f32(r(sum_s P_s)) (round) or G += sum_s P_s; with kAccStore, G = (the same). With `vec` (N and ldg multiples of
-// 4, 16-byte aligned buffers) each thread moves four columns with 16-byte accesses.
+// G[m, n] += f32(r(sum_s P_s)) (round) or G += sum_s P_s; with kAccStore, G = the same
+// sum (G not read). With `vec` (N and ldg multiples of 4, 16-byte aligned buffers) each
+// thread moves four columns with 16-byte accesses.
 static __global__ void __launch_bounds__(256) splitk_accum_kernel(const float* __restrict__ part,
                                                            int splits, long split_stride,
                                                            float* __restrict__ g, long ldg, int M,

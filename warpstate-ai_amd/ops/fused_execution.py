@@ -104,14 +104,16 @@ def dgrad_mm(grad: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
     gradient) and the BF16 weight [N, K] in nn.Linear layout; returns [M, K]
     (ops/matmul_execution.py:239).
 
-    This library's GEMM (``ws_mm``, FP32 accumulation, one BF16 rounding), with the
-    weight first copied K-contiguous by the HIP transpose kernel (``k_contiguous_b``) when
-    grad has enough rows to amortize the copy.
+    This library's GEMM (``ws_mm``, FP32 accumulation, one BF16 rounding) on the
+    persistent grid (one workgroup per CU looping over the tiles: 2.5-3.5 % faster than a
+    workgroup per tile at 16384 x 2048 x 9216 / x 11264, bit-identical), with the weight
+    first copied K-contiguous by the HIP transpose kernel (``k_contiguous_b``) when grad
+    has enough rows to amortize the copy.
     """
     _check_bf16_cuda(grad, weight)
     if grad.dim() != 2 or weight.dim() != 2 or grad.shape[1] != weight.shape[0]:
         raise ValueError("Expected grad [M, N] and weight [N, K]")
-    return mm(grad, weight)
+    return mm(grad, weight, "persistent")
 
 
 def rmsnorm_gate_mm(x: torch.Tensor, norm_weight: torch.Tensor, eps: float,
