@@ -350,7 +350,7 @@ def _fused_adapter_case(size, hip_calls):
         assert logits.shape == (*tokens, vocab)
 
 
-@pytest.mark.parametrize("variant", ["eager", "checkpointed", "compiled_cores"])
+@pytest.mark.parametrize("variant", ["eager", "checkpointed", "compiled_cores", "compiled_model"])
 def test_fused_adapter_on_the_reference_core_layout(variant, hip_calls):
     """A model in the reference's own layout (one WarpStateCore.forward with _split, the
     inline gate sigmoid and residual adds, and the inline chunked loss; no seams): the
@@ -377,8 +377,11 @@ def test_fused_adapter_on_the_reference_core_layout(variant, hip_calls):
         apply_fused_execution(actual)
         for model in (reference, actual):
             apply_bf16_residuals(model)
+        run = actual
         if variant == "compiled_cores":
             _compile_training_cores(actual, "aot_eager")
+        elif variant == "compiled_model":
+            run = torch.compile(actual, backend="aot_eager")
         gen = torch.Generator("cpu").manual_seed(12)
         inputs = torch.randint(vocab, tokens, generator=gen).cuda()
         labels = torch.randint(vocab, tokens, generator=gen)
@@ -387,7 +390,7 @@ def test_fused_adapter_on_the_reference_core_layout(variant, hip_calls):
         with torch.autocast("cuda", dtype=torch.bfloat16):
             expected = reference(inputs, labels, return_logits=False)[1]
             hip_calls.clear()
-            result = actual(inputs, labels, return_logits=False)[1]
+            result = run(inputs, labels, return_logits=False)[1]
         for name in ("ws_rmsnorm_forward", "ws_mm", "ws_swiglu_mm", "ws_linear_ce_fused"):
             assert name in hip_calls, (name, hip_calls)
         # The seams' fusions are not available here.
