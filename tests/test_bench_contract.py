@@ -43,8 +43,10 @@ def test_committed_bench_line_keeps_the_contract():
     assert roof["peak"] == 2516.6 and roof["unit"] == "TFLOP/s"
     assert abs(roof["frac"] - roof["achieved"] / roof["peak"]) < 1e-3
     assert roof["kernel"] in line["kernels"]
-    # The dominant kernel is the slowest measured region.
-    assert roof["kernel"] == max(line["kernels"], key=lambda k: line["kernels"][k]["ms"])
+    # The dominant kernel is the slowest measured region of the step. The hipBLASLt
+    # yardstick and the adapter operator are timed outside the step and do not compete.
+    step_regions = [k for k in line["kernels"] if not k.endswith((".hipblaslt", ".adapter_op"))]
+    assert roof["kernel"] == max(step_regions, key=lambda k: line["kernels"][k]["ms"])
     traffic_lines = {p[1]: int(p[2]) for p in
                      (l.split() for l in TRAFFIC.read_text().splitlines())
                      if len(p) == 3 and p[0] == "traffic_bytes"}
