@@ -83,7 +83,9 @@ int ws_rmsnorm_forward(const void* x, const float* weight, void* y, float* rstd,
 int64_t ws_rmsnorm_backward_partial_floats(int64_t rows, int64_t d);
 
 /* RMSNorm backward: dx [rows, d] BF16 and dweight [d] FP32 from x, weight, rstd and a
- * contiguous grad; replaces `_rms_backward` (ops/activation_execution.py:176-194). */
+ * contiguous grad; replaces `_rms_backward` (ops/activation_execution.py:176-194). Any
+ * width d <= 8192 and any buffer alignment (d % 8 == 0 with 16-byte aligned x, grad and dx
+ * takes the vector kernel, everything else a generic one with the same arithmetic). */
 int ws_rmsnorm_backward(const void* x, const float* weight, const float* rstd, const void* grad,
                         void* dx, float* dweight, float* partial, int64_t rows, int64_t d,
                         int eager_rounding, void* stream);

@@ -539,6 +539,65 @@ def test_standalone_rmsnorm_forward_backward(shape):
     assert rel_l2(w.grad, w_ref.grad) <= 3e-3
 
 
+@pytest.mark.parametrize("shape", [(3, 20), (5, 100), (33, 27), (9, 1001), (70, 4100),
+                                   (2, 3, 8190)])
+def test_standalone_rmsnorm_backward_any_width(shape):
+    """Widths that are not a multiple of 8 (the generic row kernel and, for odd widths, the
+    one-column-at-a-time weight reduction) against the oracle through autograd, as the
+    reference's RMSNorm takes any width."""
+    from ops.activation_execution import bf16_rmsnorm
+
+    gen = _gen(951)
+    weight = torch.rand(shape[-1], generator=gen) * 1.9 + 0.1
+    source = torch.randn(shape, generator=gen).bfloat16()
+    x_ref = source.clone().requires_grad_()
+    w_ref = weight.clone().requires_grad_()
+    expected = oracle.rmsnorm(x_ref, w_ref, 1e-5)
+    grad = torch.randn(shape, generator=gen).bfloat16()
+    expected.backward(grad)
+    x = source.cuda().requires_grad_()
+    w = weight.cuda().requires_grad_()
+    out, _rstd = bf16_rmsnorm(x, w, 1e-5, True)
+    out.backward(grad.cuda())
+    torch.cuda.synchronize()
+    assert_bf16_close(out, expected.detach(), "rmsnorm")
+    assert_bf16_close(x.grad, x_ref.grad, "rmsnorm dx")
+    assert rel_l2(w.grad, w_ref.grad) <= 3e-3
+
+
+@pytest.mark.parametrize("eager_rounding", [True, False])
+def test_rmsnorm_backward_unaligned_rows_match_aligned(eager_rounding):
+    """x and the incoming gradient as views 2 bytes past a 16-byte boundary take the generic
+    row kernel; aligned copies of the same values take the vector kernel. The weight
+    gradient sums the same values in the same order, so it is bitwise equal; dX is within
+    the oracle's bars (its row dot product is summed in another order)."""
+    from ops.activation_execution import _rms_backward
+
+    gen = _gen(955)
+    rows, d = 100, 2048
+    x = torch.randn(rows, d, generator=gen).bfloat16()
+    grad = torch.randn(rows, d, generator=gen).bfloat16()
+    weight = (torch.rand(d, generator=gen) * 1.9 + 0.1).cuda()
+    rstd = (1.0 / x.float().pow(2).mean(-1).add(1e-5).sqrt()).cuda()
+    flat_x = torch.zeros(rows * d + 8, dtype=torch.bfloat16, device="cuda")
+    flat_g = torch.zeros_like(flat_x)
+    xv = flat_x[1:1 + rows * d].view(rows, d)
+    gv = flat_g[1:1 + rows * d].view(rows, d)
+    xv.copy_(x.cuda())
+    gv.copy_(grad.cuda())
+    assert xv.data_ptr() % 16 == 2 and xv.is_contiguous() and gv.is_contiguous()
+    dx_u, dw_u = _rms_backward(xv, weight, rstd, gv, eager_rounding)
+    dx_a, dw_a = _rms_backward(x.cuda(), weight, rstd, grad.cuda(), eager_rounding)
+    torch.cuda.synchronize()
+    assert torch.equal(dw_u, dw_a)
+    assert_bf16_close(dx_u, dx_a.cpu(), "dx, unaligned against aligned")
+    if eager_rounding:
+        x_ref = x.clone().requires_grad_()
+        w_ref = weight.cpu().clone().requires_grad_()
+        oracle.rmsnorm(x_ref, w_ref, 1e-5).backward(grad)
+        assert_bf16_close(dx_u, x_ref.grad, "dx, unaligned against the oracle")
+
+
 @pytest.mark.parametrize("offset", [1, 3])
 def test_rmsnorm_forward_with_unaligned_weight_view(offset):
     """An FP32 norm weight that is a view at a 4- or 12-byte offset into a flat parameter

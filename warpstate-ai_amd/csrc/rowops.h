@@ -259,11 +259,61 @@ static __global__ void __launch_bounds__(256) rmsnorm_bwd_kernel(
         ((lds_part[c] + lds_part[D + c]) + lds_part[2 * D + c]) + lds_part[3 * D + c];
 }
 
+// The same RMSNorm backward for any width up to 8192 and any buffer alignment (rows whose
+// width is not a multiple of 8, views at odd offsets): lanes take columns lane, lane + 64,
+// ... with 2-byte loads, and each wave's weight-gradient partial builds up in its LDS row.
+// The arithmetic is the vector kernel's; the partial sums run over the block's rows in the
+// same order and the four waves are added in the same order. Only dr, each row's dot
+// product, is summed in another order (by column residue instead of by 8-column chunk).
+template <bool EAGER>
+static __global__ void __launch_bounds__(256) rmsnorm_bwd_generic_kernel(
+    const unsigned short* __restrict__ x, const float* __restrict__ w,
+    const float* __restrict__ rstd, const unsigned short* __restrict__ dy,
+    unsigned short* __restrict__ dx, float* __restrict__ dw_part, int rows, int D) {
+  extern __shared__ float lds_part[];  // [4][D]
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  float* mine = lds_part + wave * D;
+  for (int c = lane; c < D; c += 64) mine[c] = 0.0f;
+  const int row_end = min(rows, (blockIdx.x + 1) * kRmsRowsPerBlock);
+  for (int row = blockIdx.x * kRmsRowsPerBlock + wave; row < row_end; row += 4) {
+    const float r = rstd[row];
+    const unsigned short* xr = x + (long)row * D;
+    const unsigned short* gr = dy + (long)row * D;
+    float dr = 0.0f;
+    for (int c = lane; c < D; c += 64) {
+      const float wc = EAGER ? rbf16(w[c]) : w[c];
+      float dz = bf16_bits_to_f32(gr[c]) * wc;
+      if (EAGER) dz = rbf16(dz);
+      dr += dz * bf16_bits_to_f32(xr[c]);
+    }
+    dr = wave_sum(dr);
+    const float dsq = (-0.5f * dr * (r * r * r)) / (float)D;
+    for (int c = lane; c < D; c += 64) {
+      const float xs = bf16_bits_to_f32(xr[c]), gs = bf16_bits_to_f32(gr[c]);
+      const float wc = EAGER ? rbf16(w[c]) : w[c];
+      float dz = gs * wc;
+      if (EAGER) dz = rbf16(dz);
+      dx[(long)row * D + c] = to_bf16_bits(dz * r + dsq * (2.0f * xs));
+      float z = xs * r;
+      if (EAGER) z = rbf16(z);
+      float pv = gs * z;
+      if (EAGER) pv = rbf16(pv);
+      mine[c] += pv;
+    }
+  }
+  __syncthreads();
+  for (int c = threadIdx.x; c < D; c += blockDim.x)
+    dw_part[(long)blockIdx.x * D + c] =
+        ((lds_part[c] + lds_part[D + c]) + lds_part[2 * D + c]) + lds_part[3 * D + c];
+}
+
 // Column sum of the weight-gradient partials (ops/activation_execution.py:144-158). A
 // block owns 32 columns: thread (lane g, quad q) sums columns 4q..4q+3 over the partial
 // rows g, g + 32, g + 64, ... in order, then the 32 lane sums are added in a fixed
-// pairwise tree, so the result is deterministic. D % 4 == 0.
+// pairwise tree, so the result is deterministic. VEC reads the four columns as one 16-byte
+// vector (D % 4 == 0, part 16-byte aligned); otherwise one at a time, in the same order.
 constexpr int kRmsReduceCols = 32, kRmsReduceLanes = 32;
+template <bool VEC>
 static __global__ void __launch_bounds__(256) rms_weight_reduce_kernel(const float* __restrict__ part,
                                                                 float* __restrict__ dw, int groups,
                                                                 int D, int eager) {
@@ -271,10 +321,16 @@ static __global__ void __launch_bounds__(256) rms_weight_reduce_kernel(const flo
   const int q = threadIdx.x & 7, g0 = threadIdx.x >> 3;
   const int c = blockIdx.x * kRmsReduceCols + 4 * q;
   f32x4_t total = {0.0f, 0.0f, 0.0f, 0.0f};
-  if (c < D) {
+  if (VEC && c < D) {
 #pragma unroll 8
     for (int g = g0; g < groups; g += kRmsReduceLanes)
       total += *reinterpret_cast<const f32x4_t*>(part + (long)g * D + c);
+  } else if (!VEC) {
+    for (int g = g0; g < groups; g += kRmsReduceLanes) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (c + e < D) total[e] += part[(long)g * D + c + e];
+    }
   }
   sums[g0][q] = total;
   __syncthreads();
@@ -283,9 +339,10 @@ static __global__ void __launch_bounds__(256) rms_weight_reduce_kernel(const flo
     if (g0 < width) sums[g0][q] += sums[g0 + width][q];
     __syncthreads();
   }
-  if (g0 == 0 && c < D) {
+  if (g0 == 0) {
 #pragma unroll
-    for (int e = 0; e < 4; ++e) dw[c + e] = eager ? rbf16(sums[0][q][e]) : sums[0][q][e];
+    for (int e = 0; e < 4; ++e)
+      if (c + e < D) dw[c + e] = eager ? rbf16(sums[0][q][e]) : sums[0][q][e];
   }
 }
 

@@ -73,30 +73,46 @@ static int launch_rms_bwd(const void* x, const float* weight, const float* rstd,
   return eager ? launch(&rmsnorm_bwd_kernel<SEGS, true>) : launch(&rmsnorm_bwd_kernel<SEGS, false>);
 }
 
+static int launch_rms_bwd_generic(const void* x, const float* weight, const float* rstd,
+                                  const void* grad, void* dx, float* partial, int rows, int d,
+                                  int eager, hipStream_t s) {
+  const int lds = 4 * d * (int)sizeof(float);
+  auto launch = [&](auto kernel) {
+    if (int rc = ensure_lds(reinterpret_cast<const void*>(kernel), lds)) return rc;
+    hipLaunchKernelGGL(kernel, dim3(cdiv(rows, kRmsRowsPerBlock)), dim3(256), lds, s,
+                       static_cast<const unsigned short*>(x), weight, rstd,
+                       static_cast<const unsigned short*>(grad), static_cast<unsigned short*>(dx),
+                       partial, rows, d);
+    return hip_check(hipGetLastError(), "rmsnorm backward launch");
+  };
+  return eager ? launch(&rmsnorm_bwd_generic_kernel<true>) : launch(&rmsnorm_bwd_generic_kernel<false>);
+}
+
 static int rmsnorm_backward(const void* x, const float* weight, const float* rstd,
                             const void* grad, void* dx, float* dweight, float* partial,
                             int64_t rows, int64_t d, int eager_rounding, void* stream) {
   if (!x || !weight || !rstd || !grad || !dx || !dweight || !partial)
     return set_error(kInvalid, "null pointer");
   if (rows < 1 || d < 1 || !fits_i32(rows) || !fits_i32(d)) return set_error(kInvalid, "invalid RMSNorm shape");
-  if (d > 8192 || d % 8 != 0)
-    return set_error(kInvalid, "RMSNorm backward needs a width that is a multiple of 8, at most 8192 (got %ld)", (long)d);
-  const unsigned long a = reinterpret_cast<unsigned long>(x) | reinterpret_cast<unsigned long>(grad) |
-                          reinterpret_cast<unsigned long>(dx) | reinterpret_cast<unsigned long>(weight) |
-                          reinterpret_cast<unsigned long>(partial);
-  if (a % 16) return set_error(kInvalid, "RMSNorm backward needs 16-byte aligned buffers");
+  if (d > 8192) return set_error(kInvalid, "RMSNorm backward takes rows of at most 8192 columns (got %ld)", (long)d);
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int segs = cdiv(d, 512), e = eager_rounding ? 1 : 0;
+  // The vector kernels read x and grad and write dx as 16-byte pieces of 8 columns.
+  const unsigned long a = reinterpret_cast<unsigned long>(x) | reinterpret_cast<unsigned long>(grad) |
+                          reinterpret_cast<unsigned long>(dx);
   int rc;
-  if (segs <= 1) rc = launch_rms_bwd<1>(x, weight, rstd, grad, dx, partial, (int)rows, (int)d, e, s);
+  if (d % 8 != 0 || a % 16 != 0) rc = launch_rms_bwd_generic(x, weight, rstd, grad, dx, partial, (int)rows, (int)d, e, s);
+  else if (segs <= 1) rc = launch_rms_bwd<1>(x, weight, rstd, grad, dx, partial, (int)rows, (int)d, e, s);
   else if (segs <= 2) rc = launch_rms_bwd<2>(x, weight, rstd, grad, dx, partial, (int)rows, (int)d, e, s);
   else if (segs <= 4) rc = launch_rms_bwd<4>(x, weight, rstd, grad, dx, partial, (int)rows, (int)d, e, s);
   else if (segs <= 8) rc = launch_rms_bwd<8>(x, weight, rstd, grad, dx, partial, (int)rows, (int)d, e, s);
   else rc = launch_rms_bwd<16>(x, weight, rstd, grad, dx, partial, (int)rows, (int)d, e, s);
   if (rc) return rc;
   const int groups = cdiv(rows, kRmsRowsPerBlock);
-  hipLaunchKernelGGL(rms_weight_reduce_kernel, dim3(cdiv(d, kRmsReduceCols)), dim3(256), 0, s, partial,
-                     dweight, groups, (int)d, e);
+  const bool vec = d % 4 == 0 && reinterpret_cast<unsigned long>(partial) % 16 == 0;
+  hipLaunchKernelGGL(vec ? rms_weight_reduce_kernel<true> : rms_weight_reduce_kernel<false>,
+                     dim3(cdiv(d, kRmsReduceCols)), dim3(256), 0, s, partial, dweight, groups,
+                     (int)d, e);
   return hip_check(hipGetLastError(), "rmsnorm weight reduce launch");
 }
 
