@@ -357,29 +357,37 @@ def bench_extra(args, device):
     # the chunk workspace (512 MiB; the full [16384, 32768] logits never do), and the
     # chunk's dHidden is formed while they are there; the backward scales by the upstream
     # gradient. The two-pass variant (logits only in registers, recomputed by the
-    # backward) is timed beside it.
-    for key, fused, note in (
-            ("config5_lm_head_ce_16384x2048x32768", True,
+    # backward) is timed beside it. So is the one-pass loss under an upstream gradient that
+    # is not a power of two (1/3, e.g. a loss averaged over three micro-batches): its
+    # backward then falls back to the two-pass recompute, after the forward has already
+    # formed the unit gradients.
+    third = torch.full((), 1.0 / 3.0, device=device)
+    fused_state = None
+    for key, fused, g, note in (
+            ("config5_lm_head_ce_16384x2048x32768", True, one,
              "logits fwd + dHidden, one pass (ws_linear_ce_fused) + upstream scale"),
-            ("config5_two_pass_recompute_16384x2048x32768", False,
-             "logits fwd + dHidden; the backward recomputes the logits GEMM (not counted)")):
+            ("config5_two_pass_recompute_16384x2048x32768", False, one,
+             "logits fwd + dHidden; the backward recomputes the logits GEMM (not counted)"),
+            ("config5_one_pass_upstream_third_16384x2048x32768", True, third,
+             "one-pass loss with upstream gradient 1/3: the backward falls back to the "
+             "two-pass recompute (its extra GEMMs not counted)")):
         state = CrossEntropyState(M, VOCAB, device, d=D, fused=fused)
         for _ in range(args.warmup):
             linear_cross_entropy_forward(hidden, weight, targets, state)
-            linear_cross_entropy_backward(hidden, weight, targets, state, one, out=dh)
+            linear_cross_entropy_backward(hidden, weight, targets, state, g, out=dh)
         t = Timer()
         for _ in range(args.steps):
             with t.region("fwd"):
                 linear_cross_entropy_forward(hidden, weight, targets, state)
             with t.region("bwd"):
-                linear_cross_entropy_backward(hidden, weight, targets, state, one, out=dh)
+                linear_cross_entropy_backward(hidden, weight, targets, state, g, out=dh)
         torch.cuda.synchronize()
         ms = t.mean_ms("fwd") + t.mean_ms("bwd")
         res[key] = {
             "ms": round(ms, 4), "fwd_ms": round(t.mean_ms("fwd"), 4),
             "bwd_ms": round(t.mean_ms("bwd"), 4), "tflops": round(f5 / ms / 1e9, 1),
             "pct_peak": round(100 * f5 / ms / 1e9 / PEAK_BF16_TFLOPS, 2), "flops_note": note}
-        if fused:
+        if fused and fused_state is None:
             fused_state = state
         else:
             del state

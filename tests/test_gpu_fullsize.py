@@ -13,7 +13,7 @@ import math
 import pytest
 import torch
 
-from metrics import assert_bf16_close, assert_f32_close
+from metrics import assert_bf16_close, assert_f32_close, rel_l2
 from oracle import reference as oracle
 from ops import benchmark_configs as cfg
 
@@ -51,6 +51,46 @@ def test_config2_rmsnorm_gate_projection_full():
     assert torch.all(zero[:, lo:hi] == 0.5).item()
     assert torch.count_nonzero(zero[:, :lo]).item() == 0
     assert torch.count_nonzero(zero[:, hi:]).item() == 0
+
+
+def test_config2_qkv_backward_full(monkeypatch):
+    """The backward of config 2 at its full size on this library's kernels only: the
+    gate-sigmoid backward, dY = r(dP @ W) on the library's GEMM, the FP32-accumulated
+    projection weight gradient and the RMSNorm backward, against the oracle's autograd of
+    the same forward; a zero upstream gradient leaves the FP32 buffer bit for bit."""
+    from ops import _hip
+    from ops.fused_execution import rmsnorm_gate_mm, rmsnorm_gate_mm_backward
+
+    inp = cfg.rms_projection_inputs(seed=0)
+    m, d = inp["x"].shape
+    n = inp["w"].shape[0]
+    gen = torch.Generator("cpu").manual_seed(12)
+    dout = (torch.randn(m, n, generator=gen) * 1e-2).bfloat16()
+    g0 = torch.randn(n, d, generator=gen) * 1e-4
+    x, nw, w = inp["x"].cuda(), inp["norm_weight"].cuda(), inp["w"].cuda()
+    normed = torch.empty_like(x)
+    out, rstd = rmsnorm_gate_mm(x, nw, inp["eps"], w, inp["gate"], normed=normed)
+    g = g0.cuda()
+    calls, real = [], _hip.call
+    monkeypatch.setattr(_hip, "call", lambda name, *a: (calls.append(name), real(name, *a))[1])
+    dx, dnw = rmsnorm_gate_mm_backward(x, nw, rstd, normed, w, inp["gate"], out, dout.cuda(), g)
+    torch.cuda.synchronize()
+    monkeypatch.setattr(_hip, "call", real)
+    assert calls == ["ws_sigmoid_backward_cols", "ws_transpose_bf16", "ws_mm",
+                     "ws_mm_accumulate_f32", "ws_rmsnorm_backward"], calls
+    want_dx, want_dnw, want_g = oracle.rmsnorm_gate_projection_backward(
+        inp["x"], inp["norm_weight"], inp["eps"], inp["w"], inp["gate"], dout, g0)
+    assert_bf16_close(dx, want_dx, "config2 backward dX")
+    # The norm weight's gradient sums 16384 rows of BF16-rounded products (the bar of the
+    # reduced-size test of the same backward).
+    assert rel_l2(dnw, want_dnw) <= 3e-3
+    assert_f32_close(g.cpu(), want_g, "config2 backward W gradient")
+    assert_f32_close(g.cpu() - g0, want_g - g0, "config2 backward dW")
+    before = g.clone()
+    rmsnorm_gate_mm_backward(x, nw, rstd, normed, w, inp["gate"], out,
+                             torch.zeros_like(dout, device="cuda"), g)
+    torch.cuda.synchronize()
+    assert torch.equal(g, before)
 
 
 def test_config3_down_residual_full():
