@@ -38,19 +38,31 @@ int device_cus() {
   return g_cus[dev];
 }
 
-// hipFuncSetAttribute applies to the current device; remember (kernel, device) pairs.
+// hipFuncSetAttribute applies to the current device. The limit set for each (kernel,
+// device) is remembered and only ever raised: a kernel whose LDS size depends on its
+// arguments (the RMSNorm backward's [4][d] partials) may come first with a small size.
 int ensure_lds(const void* kernel, int bytes) {
+  struct Limit {
+    const void* kernel;
+    int dev;
+    int bytes;
+  };
   static std::mutex mu;
-  static std::vector<std::pair<const void*, int>>* seen = new std::vector<std::pair<const void*, int>>();
+  static std::vector<Limit>* seen = new std::vector<Limit>();
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return set_error(kHipError, "hipGetDevice failed");
   std::lock_guard<std::mutex> lock(mu);
+  Limit* entry = nullptr;
   for (auto& e : *seen)
-    if (e.first == kernel && e.second == dev) return kOk;
+    if (e.kernel == kernel && e.dev == dev) entry = &e;
+  if (entry && entry->bytes >= bytes) return kOk;
   hipError_t err = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
   if (err != hipSuccess)
     return set_error(kHipError, "hipFuncSetAttribute(%d bytes LDS): %s", bytes, hipGetErrorString(err));
-  seen->push_back({kernel, dev});
+  if (entry)
+    entry->bytes = bytes;
+  else
+    seen->push_back({kernel, dev, bytes});
   return kOk;
 }
 

@@ -13,7 +13,7 @@ enum Status { kOk = 0, kInvalid = 1, kHipError = 2 };
 
 int set_error(int code, const char* fmt, ...);  // records the thread's last error, returns code
 int device_cus();                               // compute units of the current device
-int ensure_lds(const void* kernel, int bytes);  // raises the dynamic LDS limit once per device
+int ensure_lds(const void* kernel, int bytes);  // raises the kernel's dynamic LDS limit on this device to >= bytes
 
 inline int hip_check(hipError_t e, const char* what) {
   if (e != hipSuccess) return set_error(kHipError, "%s: %s", what, hipGetErrorString(e));
