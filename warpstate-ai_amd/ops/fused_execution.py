@@ -88,6 +88,8 @@ def k_contiguous_b(b: torch.Tensor, rows_a: int) -> torch.Tensor:
 def mm(a: torch.Tensor, b: torch.Tensor, algorithm: str = "tiled", tile: int = 0) -> torch.Tensor:
     """r(a @ b) with the HIP GEMM; `tile` 0 = 256x256, 1 = 128x128."""
     _check_bf16_cuda(a, b)
+    if a.ndim != 2 or b.ndim != 2 or a.shape[1] != b.shape[0]:
+        raise ValueError(f"Expected a [M, K] and b [K, N], got {list(a.shape)} and {list(b.shape)}")
     if tile == 0:
         b = k_contiguous_b(b, a.shape[0])
     m, k = a.shape
