@@ -237,23 +237,42 @@ def bench_gpu(args):
         kernels[name] = {"ms": round(ms, 4), "tflops": round(f / ms / 1e9, 1),
                          "pct_peak": round(100 * f / ms / 1e9 / PEAK_BF16_TFLOPS, 2),
                          "flops": f}
-    # hipBLASLt (torch.mm) on the same two input-gradient products, as a yardstick for
-    # this library's plain GEMM: the same weight transpose, then the vendor GEMM, timed
-    # the same way. Not part of the step.
+    # hipBLASLt (torch.mm) as a yardstick, outside the step, timed the same way:
+    # - on the two input-gradient products, after the same weight transpose (the same
+    #   work as this library's kernels there);
+    # - on the plain product of every other GEMM region, the operands as the step holds
+    #   them, without the work this library fuses into it (RMSNorm row pass and gate
+    #   sigmoid, SwiGLU, residual add, SwiGLU backward, the FP32 accumulation of the weight
+    #   gradients: hipBLASLt writes BF16 instead).
     from ops.fused_execution import k_contiguous_b
+    from ops.matmul_epilogue import launch_swiglu_mm
 
+    packed, act = launch_swiglu_mm(inp["mlp_x"], inp["mlp_w_upgate"].T, "persistent",
+                                   (128, 128, 32, 8, 3), True)
+    products = {
+        "qkv_fwd": lambda: torch.mm(out["qkv_z"], inp["qkv_w"].T),
+        "swiglu_fwd": lambda: torch.mm(inp["mlp_x"], inp["mlp_w_upgate"].T),
+        "down_fwd": lambda: torch.mm(inp["down_h"], inp["down_w_down"].T),
+        "mlp_bwd.dact_swiglu": lambda: torch.mm(inp["mlp_dy"], inp["mlp_w_down"]),
+        "mlp_bwd.dx": lambda: torch.mm(out["dpacked"], k_contiguous_b(inp["mlp_w_upgate"], m)),
+        "mlp_bwd.wgrad": lambda: (torch.mm(inp["mlp_dy"].T, act),
+                                  torch.mm(out["dpacked"].T, inp["mlp_x"])),
+        "qkv_bwd.dx": lambda: torch.mm(inp["qkv_dp"], k_contiguous_b(inp["qkv_w"], m)),
+        "qkv_bwd.wgrad": lambda: torch.mm(inp["qkv_dp"].T, out["qkv_z"]),
+    }
     vendor = Timer()
     for _ in range(max(2, args.warmup)):  # hipBLASLt picks its kernel on a shape's first call
-        torch.mm(out["dpacked"], k_contiguous_b(inp["mlp_w_upgate"], m))
-        torch.mm(inp["qkv_dp"], k_contiguous_b(inp["qkv_w"], m))
+        for fn in products.values():
+            fn()
     for _ in range(args.steps):
-        with vendor.region("mlp_bwd.dx"):
-            torch.mm(out["dpacked"], k_contiguous_b(inp["mlp_w_upgate"], m))
-        with vendor.region("qkv_bwd.dx"):
-            torch.mm(inp["qkv_dp"], k_contiguous_b(inp["qkv_w"], m))
+        for name, fn in products.items():
+            with vendor.region(name):
+                fn()
     torch.cuda.synchronize()
-    for name in ("mlp_bwd.dx", "qkv_bwd.dx"):
-        ms, f = vendor.mean_ms(name), sub[name]
+    plain = {"qkv_fwd": 2 * m * NQKV * D, "swiglu_fwd": 2 * m * 2 * FFN * D,
+             "down_fwd": 2 * m * D * FFN, **sub}
+    for name in products:
+        ms, f = vendor.mean_ms(name), plain[name]
         kernels[name + ".hipblaslt"] = {"ms": round(ms, 4), "tflops": round(f / ms / 1e9, 1),
                                         "pct_peak": round(100 * f / ms / 1e9 / PEAK_BF16_TFLOPS, 2),
                                         "flops": f}
@@ -261,10 +280,7 @@ def bench_gpu(args):
     # as mlp_bwd, with the two weight gradients written into fresh FP32 buffers (returned
     # through autograd) instead of accumulated into resident ones.
     from ops.fused_training import fused_swiglu_block_backward
-    from ops.matmul_epilogue import launch_swiglu_mm
 
-    packed, act = launch_swiglu_mm(inp["mlp_x"], inp["mlp_w_upgate"].T, "persistent",
-                                   (128, 128, 32, 8, 3), True)
     adapter = Timer()
     for i in range(args.warmup + args.steps):
         with adapter.region("run" if i >= args.warmup else "warm"):
