@@ -598,6 +598,45 @@ def test_rmsnorm_backward_unaligned_rows_match_aligned(eager_rounding):
         assert_bf16_close(dx_u, x_ref.grad, "dx, unaligned against the oracle")
 
 
+def test_forward_weights_stored_k_by_n_match_the_native_layout(monkeypatch):
+    """Forward weights stored [K, N] row-major (the reference's second measured layout, an
+    N-contiguous B) are copied K-contiguous by the transpose kernel before the fused
+    projections, and give the native [N, K] layout's bits: the RMSNorm-prologue projection,
+    the residual projection and the paired SwiGLU projection."""
+    from ops import _hip
+    from ops.fused_execution import residual_mm, rmsnorm_gate_mm
+    from ops.matmul_epilogue import launch_swiglu_mm
+
+    gen = _gen(957)
+    m, k, n = 1024, 384, 640
+    x = torch.randn(m, k, generator=gen).bfloat16().cuda()
+    nw = (torch.rand(k, generator=gen) * 1.9 + 0.1).cuda()
+    w = (torch.randn(n, k, generator=gen) * 0.05).bfloat16().cuda()
+    r = torch.randn(m, n, generator=gen).bfloat16().cuda()
+    w_kn = w.T.contiguous()
+    calls, real = [], _hip.call
+    monkeypatch.setattr(_hip, "call", lambda name, *a: (calls.append(name), real(name, *a))[1])
+    pairs = [
+        (lambda: rmsnorm_gate_mm(x, nw, 1e-6, w, (128, 256))[0],
+         lambda: rmsnorm_gate_mm(x, nw, 1e-6, w_kn.T, (128, 256))[0], "ws_rmsnorm_gate_mm"),
+        (lambda: residual_mm(x, w, r), lambda: residual_mm(x, w_kn.T, r), "ws_residual_mm"),
+        (lambda: launch_swiglu_mm(x, w.T, "persistent", (128, 128, 32, 8, 3), True),
+         lambda: launch_swiglu_mm(x, w_kn, "persistent", (128, 128, 32, 8, 3), True),
+         "ws_swiglu_mm"),
+    ]
+    for native, stored_kn, entry in pairs:
+        calls.clear()
+        want = native()
+        assert calls == [entry], calls
+        calls.clear()
+        got = stored_kn()
+        assert calls == ["ws_transpose_bf16", entry], calls
+        torch.cuda.synchronize()
+        for g, e in zip(got if isinstance(got, tuple) else (got,),
+                        want if isinstance(want, tuple) else (want,)):
+            assert torch.equal(g, e), entry
+
+
 @pytest.mark.parametrize("offset", [1, 3])
 def test_rmsnorm_forward_with_unaligned_weight_view(offset):
     """An FP32 norm weight that is a view at a 4- or 12-byte offset into a flat parameter

@@ -77,8 +77,9 @@ def transpose(x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
 
 def k_contiguous_b(b: torch.Tensor, rows_a: int) -> torch.Tensor:
     """B [K, N] as a view whose reduction dim is contiguous: when B is N-contiguous (a
-    weight in an input-gradient GEMM, dX = dY @ W) and A has enough rows to amortize it,
-    a transposed copy W^T [N, K] viewed as [K, N]; otherwise B itself."""
+    weight in an input-gradient GEMM, dX = dY @ W, or a forward weight stored [K, N]
+    row-major) and A has enough rows to amortize it, a transposed copy W^T [N, K] viewed
+    as [K, N]; otherwise B itself. The copy is exact, so results are the same bits."""
     if (rows_a >= TRANSPOSE_MIN_ROWS and b.stride(1) == 1 and b.stride(0) >= b.shape[1]
             and b.shape[0] > 1):
         return transpose(b).T
@@ -152,7 +153,8 @@ def rmsnorm_gate_mm(x: torch.Tensor, norm_weight: torch.Tensor, eps: float,
     if normed is None:
         normed = torch.empty((m, k), dtype=torch.bfloat16, device=x.device)
     _check_buffer(normed, (m, k), torch.bfloat16, x.device, "normed")
-    b = weight.T
+    # A weight stored [K, N] (N-contiguous B) is copied K-contiguous first, as for dX.
+    b = k_contiguous_b(weight.T, m)
     _hip.call("ws_rmsnorm_gate_mm", x.data_ptr(), x.stride(0), norm_weight.data_ptr(),
               float(eps), rstd.data_ptr(), normed.data_ptr(), b.data_ptr(), b.stride(0),
               b.stride(1), out.data_ptr(), m, n, k, int(gate[0]), int(gate[1]), _hip.stream(x))
@@ -211,7 +213,7 @@ def residual_mm(a: torch.Tensor, weight: torch.Tensor, residual: torch.Tensor,
     if out is None:
         out = torch.empty((m, n), dtype=torch.bfloat16, device=a.device)
     _check_buffer(out, (m, n), torch.bfloat16, a.device, "out")
-    b = weight.T
+    b = k_contiguous_b(weight.T, m)
     _hip.call("ws_residual_mm", a.data_ptr(), a.stride(0), a.stride(1), b.data_ptr(),
               b.stride(0), b.stride(1), residual.data_ptr(), residual.stride(0),
               out.data_ptr(), m, n, k, _hip.stream(a))
