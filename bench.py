@@ -343,7 +343,8 @@ def bench_layout(args, device):
 
 
 def bench_extra(args, device):
-    """Configs 1 and 5, each timed over `steps` launches with HIP events."""
+    """Configs 1 and 5, and configs 1-3 with weights stored [K, N], each timed over `steps`
+    launches with HIP events."""
     from ops.benchmark_configs import lm_head_inputs, swiglu_forward_inputs
     from ops.fused_execution import (CrossEntropyState, linear_cross_entropy_backward,
                                      linear_cross_entropy_forward)
@@ -363,7 +364,54 @@ def bench_extra(args, device):
     ms = t.mean_ms("c1")
     res["config1_swiglu_4096x1024x5632"] = {"ms": round(ms, 4), "tflops": round(f1 / ms / 1e9, 1),
                                             "pct_peak": round(100 * f1 / ms / 1e9 / PEAK_BF16_TFLOPS, 2)}
-    del x, w
+    # Configs 1-3 with the weight stored [K, N] row-major, the reference's second measured
+    # layout (an N-contiguous B; the launchers copy it K-contiguous first). Configs 2 and 3
+    # in the native layout are the step's qkv_fwd and down_fwd regions.
+    from ops.benchmark_configs import down_residual_inputs, rms_projection_inputs
+    from ops.fused_execution import residual_mm, rmsnorm_gate_mm
+
+    w_kn = w.T.contiguous()
+    c2 = rms_projection_inputs(seed=0)
+    x2, nw2, w2_kn = c2["x"].to(device), c2["norm_weight"].to(device), c2["w"].to(device).T.contiguous()
+    c3 = down_residual_inputs(seed=0)
+    h3, r3, w3_kn = c3["h"].to(device), c3["residual"].to(device), c3["w_down"].to(device).T.contiguous()
+    o2 = torch.empty((M, NQKV), dtype=torch.bfloat16, device=device)
+    rs2 = torch.empty((M,), dtype=torch.float32, device=device)
+    z2 = torch.empty((M, D), dtype=torch.bfloat16, device=device)
+    o3 = torch.empty((M, D), dtype=torch.bfloat16, device=device)
+    w2, w3 = c2["w"].to(device), c3["w_down"].to(device)
+    kn = {  # (FLOPs, native-layout call, [K, N]-layout call), alternated call by call
+        "config1_swiglu_4096x1024x5632_kn_weight": (
+            f1, lambda: launch_swiglu_mm(x, w.T, "persistent", (128, 128, 32, 8, 3), True),
+            lambda: launch_swiglu_mm(x, w_kn, "persistent", (128, 128, 32, 8, 3), True)),
+        "config2_rmsnorm_qkv_16384x2048x9216_kn_weight": (
+            2 * M * NQKV * D,
+            lambda: rmsnorm_gate_mm(x2, nw2, c2["eps"], w2, c2["gate"], out=o2, rstd=rs2,
+                                    normed=z2),
+            lambda: rmsnorm_gate_mm(x2, nw2, c2["eps"], w2_kn.T, c2["gate"], out=o2, rstd=rs2,
+                                    normed=z2)),
+        "config3_down_residual_16384x5632x2048_kn_weight": (
+            2 * M * D * FFN, lambda: residual_mm(h3, w3, r3, out=o3),
+            lambda: residual_mm(h3, w3_kn.T, r3, out=o3)),
+    }
+    for key, (f, native, stored_kn) in kn.items():
+        for _ in range(args.warmup):
+            native()
+            stored_kn()
+        t = Timer()
+        for _ in range(args.steps):
+            with t.region("native"):
+                native()
+            with t.region("kn"):
+                stored_kn()
+        torch.cuda.synchronize()
+        ms, ms_native = t.mean_ms("kn"), t.mean_ms("native")
+        res[key] = {"ms": round(ms, 4), "tflops": round(f / ms / 1e9, 1),
+                    "pct_peak": round(100 * f / ms / 1e9 / PEAK_BF16_TFLOPS, 2),
+                    "native_layout_ms": round(ms_native, 4),
+                    "flops_note": "weight stored [K, N]; its K-contiguous copy is timed; the "
+                                  "native [N, K] layout alternated with it call by call"}
+    del x, w, w_kn, x2, nw2, w2, w2_kn, h3, r3, w3, w3_kn, o2, rs2, z2, o3
     c5 = lm_head_inputs(seed=0)
     hidden, weight, targets = (c5[k].to(device) for k in ("hidden", "weight", "targets"))
     dh = torch.empty((M, D), dtype=torch.bfloat16, device=device)
