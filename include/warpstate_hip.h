@@ -79,7 +79,8 @@ int ws_swiglu_backward(const void* packed, const void* grad, void* out, int64_t 
 int ws_rmsnorm_forward(const void* x, const float* weight, void* y, float* rstd, int64_t rows,
                        int64_t d, float eps, int eager_rounding, void* stream);
 
-/* Floats of the `partial` workspace ws_rmsnorm_backward needs. */
+/* Floats of the `partial` workspace ws_rmsnorm_backward needs: one partial row of d floats
+ * per 32 rows up to d = 2048, per 4 to 32 rows (depending on the row count) above. */
 int64_t ws_rmsnorm_backward_partial_floats(int64_t rows, int64_t d);
 
 /* RMSNorm backward: dx [rows, d] BF16 and dweight [d] FP32 from x, weight, rstd and a
@@ -94,8 +95,8 @@ int ws_rmsnorm_backward(const void* x, const float* weight, const float* rstd, c
  * weight-gradient partials in a static 4 MiB device array of the library instead of a
  * caller workspace. No counterpart in the reference: it is for callers that cannot
  * allocate (code under HIP graph capture, tight serving loops, harnesses that forbid
- * hipMalloc). It calls no allocator. Limits: d <= 4096 (wider rows take a kernel that
- * spills to runtime-allocated private memory) and ceil(rows / 32) * d <=
+ * hipMalloc). It calls no allocator, and none of its row kernels uses runtime-allocated
+ * private memory. Limits: d <= 8192 and ws_rmsnorm_backward_partial_floats(rows, d) <=
  * ws_rmsnorm_backward_static_max_partial_floats() (2^20; e.g. 16384 x 2048); larger
  * sizes return an error. Each GPU holds its own copy of the array until the process
  * ends; calls that overlap on one GPU share it and race. */

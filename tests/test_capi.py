@@ -135,10 +135,20 @@ def test_grouped_fallback_splits_follow_auto_splits():
 
 
 def test_static_rmsnorm_backward_refuses_wide_rows_before_any_launch():
-    """The allocation-free RMSNorm backward takes rows of at most 4096 columns: wider rows
-    need a kernel that spills to private memory the runtime would allocate. The check runs
-    before any device call."""
+    """The allocation-free RMSNorm backward takes rows of at most 8192 columns, the widest
+    any of its row kernels takes. The check runs before any device call."""
     gpu_ptr = 1 << 20  # never dereferenced
-    with pytest.raises(RuntimeError, match="at most 4096 columns"):
+    with pytest.raises(RuntimeError, match="at most 8192 columns"):
         _hip.call("ws_rmsnorm_backward_static", gpu_ptr, gpu_ptr, gpu_ptr, gpu_ptr, gpu_ptr,
-                  gpu_ptr, 8, 4104, 1, None)
+                  gpu_ptr, 8, 8200, 1, None)
+
+
+def test_rmsnorm_backward_partial_rows_per_width():
+    """Partial weight-gradient rows: one per 32 rows up to 2048 columns; wider rows take one
+    block per row with 4 to 32 rows per block, the most that leaves at least 512 blocks."""
+    q = lambda rows, d: _hip.query("ws_rmsnorm_backward_partial_floats", rows, d)
+    assert q(16384, 2048) == 512 * 2048 and q(33, 100) == 2 * 100
+    assert q(16384, 4096) == 512 * 4096   # 32 rows per block
+    assert q(4096, 8192) == 512 * 8192    # 8 rows per block
+    assert q(1000, 2056) == 250 * 2056    # 4 rows per block (fewer than 512 blocks)
+    assert q(65536, 4096) == 2048 * 4096  # 32 rows per block

@@ -3,10 +3,12 @@
 
 ``ws_rmsnorm_backward_static`` promises to call no allocator. A kernel that spills
 registers to private scratch memory makes the HIP runtime provide that memory at launch,
-so every kernel the static path can launch must use none: the vector row kernels for
-widths up to 4096 (1, 2, 4 and 8 segments of 512 columns), the generic row kernel (widths
-that are not a multiple of 8, unaligned views), each in both rounding modes, and both forms
-of the weight reduction. The compiler's resource remarks for ``rowops.hip``, built with the library's
+so every kernel the static path can launch must use none: for rows of up to 2048 columns
+the vector row kernels (1, 2 and 4 segments of 512 columns) and the generic row kernel
+(widths that are not a multiple of 8, unaligned views); for wider rows, up to 8192, the
+block-per-row vector kernels (2 and 4 chunks of 2048 columns) and generic kernels (16 and
+32 columns per thread); each in both rounding modes; and both forms of the weight
+reduction. The compiler's resource remarks for ``rowops.hip``, built with the library's
 flags, give each kernel's scratch bytes per lane.
 """
 import re
@@ -53,7 +55,10 @@ def test_static_rmsnorm_backward_kernels_use_no_private_scratch(tmp_path):
     scratch = _scratch_by_kernel("rowops.hip", tmp_path)
     # rmsnorm_bwd_kernel<SEGS, EAGER>: mangled as ...rmsnorm_bwd_kernelILi<SEGS>ELb<0|1>E...
     static_path = [k for k in scratch
-                   if re.search(r"rmsnorm_bwd_kernelILi(1|2|4|8)ELb[01]E", k)
-                   or "rmsnorm_bwd_generic_kernel" in k or "rms_weight_reduce_kernel" in k]
-    assert len(static_path) == 12, sorted(scratch)
+                   if re.search(r"rmsnorm_bwd_kernelILi(1|2|4)ELb[01]E", k)
+                   or "rmsnorm_bwd_generic_kernel" in k
+                   or re.search(r"rmsnorm_bwd_wide_kernelILi(2|4)ELb[01]E", k)
+                   or re.search(r"rmsnorm_bwd_wide_generic_kernelILi(16|32)ELb[01]E", k)
+                   or "rms_weight_reduce_kernel" in k]
+    assert len(static_path) == 18, sorted(scratch)
     assert {k: scratch[k] for k in static_path if scratch[k]} == {}

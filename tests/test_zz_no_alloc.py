@@ -46,7 +46,8 @@ def _workspace(x, w, rstd, dy, eager):
 
 @pytest.mark.parametrize("eager", [True, False])
 def test_static_scratch_matches_workspace_entry_point_twice(eager):
-    shapes = [(16384, 2048), (1000, 1024)]  # the second call is smaller
+    # Each call smaller than the one before; the second takes the wide-row kernel.
+    shapes = [(16384, 2048), (600, 6000), (1000, 1024)]
     for index, (rows, d) in enumerate(shapes):
         x, w, dy = _inputs(rows, d, 31 + index)
         gx, gw, gdy = x.cuda(), w.cuda(), dy.cuda()
@@ -56,7 +57,7 @@ def test_static_scratch_matches_workspace_entry_point_twice(eager):
         torch.cuda.synchronize()
         assert torch.equal(got_dx, want_dx), (rows, d)
         assert torch.equal(got_dw, want_dw), (rows, d)
-        if index == 1 and eager:
+        if index == 2 and eager:
             xl = x.clone().requires_grad_(True)
             wl = w.clone().requires_grad_(True)
             y = oracle.rmsnorm(xl, wl, 1e-6)
@@ -70,7 +71,8 @@ def test_static_scratch_rejects_sizes_beyond_its_limit():
 
     limit = _hip.query("ws_rmsnorm_backward_static_max_partial_floats")
     assert limit == 1 << 20
-    rows, d = 32 * (limit // 4096 + 1), 4096  # ceil(rows / 32) * d > limit
+    rows, d = 32 * (limit // 2048 + 1), 2048  # ceil(rows / 32) * d > limit
+    assert _hip.query("ws_rmsnorm_backward_partial_floats", rows, d) > limit
     x = torch.zeros((rows, d), dtype=torch.bfloat16, device="cuda")
     w = torch.ones(d, device="cuda")
     rstd = torch.ones(rows, device="cuda")

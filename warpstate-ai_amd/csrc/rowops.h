@@ -143,10 +143,11 @@ static __global__ void __launch_bounds__(256) rmsnorm_fwd_kernel(const unsigned 
 // RMSNorm backward (ops/activation_execution.py:113-141): per row
 //   z = r?(x r), dz = r?(dy r?(w)), dr = sum(dz x), dx = dz r + (-0.5 dr r^3 / D) * 2x,
 // and the weight-gradient partial sum over this block's rows of r?(dy z) (r? = BF16
-// rounding when eager). One wave per row, 16-byte loads: lane l owns columns
-// 8 l + 512 s (s < SEGS), and keeps its x and dy chunks in registers between the two
-// passes over the row. A block of 4 waves takes kRmsRowsPerBlock consecutive rows and writes
-// one partial weight-gradient row (summed across its waves in LDS).
+// rounding when eager). Rows of up to 2048 columns: one wave per row, 16-byte loads: lane
+// l owns columns 8 l + 512 s (s < SEGS), and keeps its x and dy chunks in registers between
+// the two passes over the row. A block of 4 waves takes kRmsRowsPerBlock consecutive rows
+// and writes one partial weight-gradient row (summed across its waves in LDS). Wider rows
+// take the block-per-row kernels below.
 constexpr int kRmsRowsPerBlock = 32;
 
 // EAGER (the rounding mode) is a template argument: tested at run time, the compiler computes
@@ -259,8 +260,8 @@ static __global__ void __launch_bounds__(256) rmsnorm_bwd_kernel(
         ((lds_part[c] + lds_part[D + c]) + lds_part[2 * D + c]) + lds_part[3 * D + c];
 }
 
-// The same RMSNorm backward for any width up to 8192 and any buffer alignment (rows whose
-// width is not a multiple of 8, views at odd offsets): lanes take columns lane, lane + 64,
+// The same RMSNorm backward for rows of up to 2048 columns with any width and alignment
+// (rows whose width is not a multiple of 8, views at odd offsets): lanes take columns lane, lane + 64,
 // ... with 2-byte loads, and each wave's weight-gradient partial builds up in its LDS row.
 // The arithmetic is the vector kernel's; the partial sums run over the block's rows in the
 // same order and the four waves are added in the same order. Only dr, each row's dot
@@ -305,6 +306,179 @@ static __global__ void __launch_bounds__(256) rmsnorm_bwd_generic_kernel(
   for (int c = threadIdx.x; c < D; c += blockDim.x)
     dw_part[(long)blockIdx.x * D + c] =
         ((lds_part[c] + lds_part[D + c]) + lds_part[2 * D + c]) + lds_part[3 * D + c];
+}
+
+// The RMSNorm backward of rows wider than 2048 columns (same arithmetic): a block of 256
+// threads takes `rpb` consecutive rows one at a time. Each thread holds its own columns of
+// the row; the row's dot product dr is summed per thread, across each wave's lanes and then
+// over the four waves (in that order, through LDS); each thread keeps its columns'
+// weight-gradient partials in registers over the block's rows (summed in row order) and
+// writes them once as the block's partial row. `rpb` (rows per block) is chosen by the
+// host from the row count, so that a call has enough blocks to fill the GPU.
+
+// The four waves' lane sums of one row, added in wave order. `red` holds two rows' slots
+// (row parity), so one barrier per row suffices: a wave writes a row's slot only after the
+// barrier of the previous row, which every wave passes only after reading the slot of the
+// row before that.
+__device__ __forceinline__ float rms_block_sum(float v, float (*red)[4], int parity, int lane,
+                                               int wave) {
+  v = wave_sum(v);
+  if (lane == 0) red[parity][wave] = v;
+  __syncthreads();
+  return ((red[parity][0] + red[parity][1]) + red[parity][2]) + red[parity][3];
+}
+
+// Wide rows whose width is a multiple of 8, 16-byte aligned x, dy and dx: thread t holds the
+// 8-column chunks starting at 8 t + 2048 v (v < V, D <= 2048 V) as 16-byte vectors, and
+// the next row's chunks are requested before the current row is reduced. EAGER (the
+// rounding mode) is a template argument: tested at run time, the compiler computes every
+// element both ways and selects.
+template <int V, bool EAGER>
+static __global__ void __launch_bounds__(256) rmsnorm_bwd_wide_kernel(
+    const unsigned short* __restrict__ x, const float* __restrict__ w,
+    const float* __restrict__ rstd, const unsigned short* __restrict__ dy,
+    unsigned short* __restrict__ dx, float* __restrict__ dw_part, int rows, int D,
+    int rpb) {
+  __shared__ float red[2][4];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  float wb[V][8], part[V][8];
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    const int c = 8 * threadIdx.x + 2048 * v;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float wv = c + e < D ? w[c + e] : 0.0f;
+      wb[v][e] = EAGER ? rbf16(wv) : wv;
+      part[v][e] = 0.0f;
+    }
+  }
+  const int r0 = blockIdx.x * rpb, r1 = min(rows, r0 + rpb);
+  auto load = [&](int row, u32x4_t (&xv)[V], u32x4_t (&gv)[V], float& rv) {
+    const bool live = row < r1;
+    rv = live ? rstd[row] : 0.0f;
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      const int c = 8 * threadIdx.x + 2048 * v;
+      const bool ok = live && c < D;
+      xv[v] = ok ? *reinterpret_cast<const u32x4_t*>(x + (long)row * D + c) : u32x4_t{0u, 0u, 0u, 0u};
+      gv[v] = ok ? *reinterpret_cast<const u32x4_t*>(dy + (long)row * D + c) : u32x4_t{0u, 0u, 0u, 0u};
+    }
+  };
+  auto reduce_row = [&](int row, const u32x4_t (&xv)[V], const u32x4_t (&gv)[V], float r) {
+    float dz[V][8];
+    float d = 0.0f;
+#pragma unroll
+    for (int v = 0; v < V; ++v)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        float dz0 = lo_bf16(gv[v][q]) * wb[v][2 * q], dz1 = hi_bf16(gv[v][q]) * wb[v][2 * q + 1];
+        if (EAGER) { dz0 = rbf16(dz0); dz1 = rbf16(dz1); }
+        dz[v][2 * q] = dz0;
+        dz[v][2 * q + 1] = dz1;
+        d += dz0 * lo_bf16(xv[v][q]);
+        d += dz1 * hi_bf16(xv[v][q]);
+      }
+    const float dr = rms_block_sum(d, red, row & 1, lane, wave);
+    const float dsq = (-0.5f * dr * (r * r * r)) / (float)D;
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      const int c = 8 * threadIdx.x + 2048 * v;
+      u32x4_t o;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        float v2[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const float xs = h ? hi_bf16(xv[v][q]) : lo_bf16(xv[v][q]);
+          const float gs = h ? hi_bf16(gv[v][q]) : lo_bf16(gv[v][q]);
+          v2[h] = dz[v][2 * q + h] * r + dsq * (2.0f * xs);
+          float z = xs * r;
+          if (EAGER) z = rbf16(z);
+          float pv = gs * z;
+          if (EAGER) pv = rbf16(pv);
+          part[v][2 * q + h] += pv;
+        }
+        o[q] = pack_bf16x2(v2[0], v2[1]);
+      }
+      if (c < D && row < r1) *reinterpret_cast<u32x4_t*>(dx + (long)row * D + c) = o;
+    }
+  };
+  // Two row buffers, used alternately (the loop takes rows in pairs, so each buffer keeps
+  // a fixed register name).
+  u32x4_t xa[V], ga[V], xb[V], gb[V];
+  float ra, rb;
+  load(r0, xa, ga, ra);
+  for (int row = r0; row < r1; row += 2) {
+    load(row + 1, xb, gb, rb);
+    reduce_row(row, xa, ga, ra);
+    if (row + 1 >= r1) break;  // uniform over the block
+    load(row + 2, xa, ga, ra);
+    reduce_row(row + 1, xb, gb, rb);
+  }
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    const int c = 8 * threadIdx.x + 2048 * v;
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      if (c + e < D) dw_part[(long)blockIdx.x * D + c + e] = part[v][e];
+  }
+}
+
+// The same for wide rows of any width up to 8192 and any buffer alignment (rows whose
+// width is not a multiple of 8, views at odd offsets): thread t takes columns t, t + 256,
+// ... (J per thread, D <= 256 J) with 2-byte accesses. The arithmetic and the order of the
+// weight-gradient sums are the vector kernel's; only dr, each row's dot product, is summed
+// in another order within each thread (by column residue instead of by 8-column chunk).
+template <int J, bool EAGER>
+static __global__ void __launch_bounds__(256) rmsnorm_bwd_wide_generic_kernel(
+    const unsigned short* __restrict__ x, const float* __restrict__ w,
+    const float* __restrict__ rstd, const unsigned short* __restrict__ dy,
+    unsigned short* __restrict__ dx, float* __restrict__ dw_part, int rows, int D,
+    int rpb) {
+  __shared__ float red[2][4];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  float wb[J], part[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const int c = threadIdx.x + 256 * j;
+    const float wv = c < D ? w[c] : 0.0f;
+    wb[j] = EAGER ? rbf16(wv) : wv;
+    part[j] = 0.0f;
+  }
+  const int r0 = blockIdx.x * rpb, r1 = min(rows, r0 + rpb);
+  for (int row = r0; row < r1; ++row) {
+    const float r = rstd[row];
+    const unsigned short* xr = x + (long)row * D;
+    const unsigned short* gr = dy + (long)row * D;
+    float xs[J], gs[J], dz[J];
+    float d = 0.0f;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const int c = threadIdx.x + 256 * j;
+      xs[j] = c < D ? bf16_bits_to_f32(xr[c]) : 0.0f;
+      gs[j] = c < D ? bf16_bits_to_f32(gr[c]) : 0.0f;
+      dz[j] = gs[j] * wb[j];
+      if (EAGER) dz[j] = rbf16(dz[j]);
+      d += dz[j] * xs[j];
+    }
+    const float dr = rms_block_sum(d, red, row & 1, lane, wave);
+    const float dsq = (-0.5f * dr * (r * r * r)) / (float)D;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const int c = threadIdx.x + 256 * j;
+      float z = xs[j] * r;
+      if (EAGER) z = rbf16(z);
+      float pv = gs[j] * z;
+      if (EAGER) pv = rbf16(pv);
+      part[j] += pv;
+      if (c < D) dx[(long)row * D + c] = to_bf16_bits(dz[j] * r + dsq * (2.0f * xs[j]));
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const int c = threadIdx.x + 256 * j;
+    if (c < D) dw_part[(long)blockIdx.x * D + c] = part[j];
+  }
 }
 
 // Column sum of the weight-gradient partials (ops/activation_execution.py:144-158). A

@@ -54,8 +54,19 @@ extern "C" int ws_rmsnorm_forward(const void* x, const float* weight, void* y, f
   return hip_check(hipGetLastError(), "rmsnorm forward launch");
 }
 
+// Rows per block of the RMSNorm backward: 32 for rows of up to 2048 columns (4 waves, one
+// row each at a time); for wider rows (one row per block at a time) the largest power of two
+// from 4 to 32 that still gives at least 512 blocks (measured against 256 and 1024 at
+// 4096 to 8192 columns: 512 blocks was fastest or tied at every shape).
+static int rms_rows_per_block(int64_t rows, int64_t d) {
+  if (d <= 2048) return kRmsRowsPerBlock;
+  int rpb = 4;
+  while (rpb < 32 && rows / (2 * rpb) >= 512) rpb *= 2;
+  return rpb;
+}
+
 extern "C" int64_t ws_rmsnorm_backward_partial_floats(int64_t rows, int64_t d) {
-  return (int64_t)cdiv(rows, kRmsRowsPerBlock) * d;
+  return (int64_t)cdiv(rows, rms_rows_per_block(rows, d)) * d;
 }
 
 template <int SEGS>
@@ -70,22 +81,37 @@ static int launch_rms_bwd(const void* x, const float* weight, const float* rstd,
                        partial, rows, d);
     return hip_check(hipGetLastError(), "rmsnorm backward launch");
   };
-  return eager ? launch(&rmsnorm_bwd_kernel<SEGS, true>) : launch(&rmsnorm_bwd_kernel<SEGS, false>);
+  if constexpr (SEGS == 0)
+    return eager ? launch(&rmsnorm_bwd_generic_kernel<true>) : launch(&rmsnorm_bwd_generic_kernel<false>);
+  else
+    return eager ? launch(&rmsnorm_bwd_kernel<SEGS, true>) : launch(&rmsnorm_bwd_kernel<SEGS, false>);
 }
 
-static int launch_rms_bwd_generic(const void* x, const float* weight, const float* rstd,
-                                  const void* grad, void* dx, float* partial, int rows, int d,
-                                  int eager, hipStream_t s) {
-  const int lds = 4 * d * (int)sizeof(float);
-  auto launch = [&](auto kernel) {
-    if (int rc = ensure_lds(reinterpret_cast<const void*>(kernel), lds)) return rc;
-    hipLaunchKernelGGL(kernel, dim3(cdiv(rows, kRmsRowsPerBlock)), dim3(256), lds, s,
-                       static_cast<const unsigned short*>(x), weight, rstd,
-                       static_cast<const unsigned short*>(grad), static_cast<unsigned short*>(dx),
-                       partial, rows, d);
-    return hip_check(hipGetLastError(), "rmsnorm backward launch");
+template <typename Kernel>
+static int launch_rms_bwd_wide(Kernel kernel, const void* x, const float* weight,
+                               const float* rstd, const void* grad, void* dx, float* partial,
+                               int rows, int d, int rpb, hipStream_t s) {
+  hipLaunchKernelGGL(kernel, dim3(cdiv(rows, rpb)), dim3(256), 0, s,
+                     static_cast<const unsigned short*>(x), weight, rstd,
+                     static_cast<const unsigned short*>(grad), static_cast<unsigned short*>(dx),
+                     partial, rows, d, rpb);
+  return hip_check(hipGetLastError(), "rmsnorm backward launch");
+}
+
+// The row kernels for a width. Up to 2048 columns: one wave per row, the vector kernel
+// (SEGS 512-column segments) when d % 8 == 0 and x, grad and dx are 16-byte aligned, else
+// the generic one. Wider rows: one block per row, the vector kernel (V 2048-column chunks)
+// or the generic one (J columns per thread).
+template <bool EAGER>
+static int rms_bwd_wide(const void* x, const float* weight, const float* rstd, const void* grad,
+                        void* dx, float* partial, int rows, int d, bool vec, hipStream_t s) {
+  const int rpb = rms_rows_per_block(rows, d);
+  auto run = [&](auto kernel) {
+    return launch_rms_bwd_wide(kernel, x, weight, rstd, grad, dx, partial, rows, d, rpb, s);
   };
-  return eager ? launch(&rmsnorm_bwd_generic_kernel<true>) : launch(&rmsnorm_bwd_generic_kernel<false>);
+  if (vec) return d <= 4096 ? run(&rmsnorm_bwd_wide_kernel<2, EAGER>) : run(&rmsnorm_bwd_wide_kernel<4, EAGER>);
+  return d <= 4096 ? run(&rmsnorm_bwd_wide_generic_kernel<16, EAGER>)
+                   : run(&rmsnorm_bwd_wide_generic_kernel<32, EAGER>);
 }
 
 static int rmsnorm_backward(const void* x, const float* weight, const float* rstd,
@@ -96,21 +122,24 @@ static int rmsnorm_backward(const void* x, const float* weight, const float* rst
   if (rows < 1 || d < 1 || !fits_i32(rows) || !fits_i32(d)) return set_error(kInvalid, "invalid RMSNorm shape");
   if (d > 8192) return set_error(kInvalid, "RMSNorm backward takes rows of at most 8192 columns (got %ld)", (long)d);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const int segs = cdiv(d, 512), e = eager_rounding ? 1 : 0;
+  const int e = eager_rounding ? 1 : 0;
   // The vector kernels read x and grad and write dx as 16-byte pieces of 8 columns.
   const unsigned long a = reinterpret_cast<unsigned long>(x) | reinterpret_cast<unsigned long>(grad) |
                           reinterpret_cast<unsigned long>(dx);
+  const bool vec = d % 8 == 0 && a % 16 == 0;
+  const int r = (int)rows, w = (int)d, segs = cdiv(d, 512);
   int rc;
-  if (d % 8 != 0 || a % 16 != 0) rc = launch_rms_bwd_generic(x, weight, rstd, grad, dx, partial, (int)rows, (int)d, e, s);
-  else if (segs <= 1) rc = launch_rms_bwd<1>(x, weight, rstd, grad, dx, partial, (int)rows, (int)d, e, s);
-  else if (segs <= 2) rc = launch_rms_bwd<2>(x, weight, rstd, grad, dx, partial, (int)rows, (int)d, e, s);
-  else if (segs <= 4) rc = launch_rms_bwd<4>(x, weight, rstd, grad, dx, partial, (int)rows, (int)d, e, s);
-  else if (segs <= 8) rc = launch_rms_bwd<8>(x, weight, rstd, grad, dx, partial, (int)rows, (int)d, e, s);
-  else rc = launch_rms_bwd<16>(x, weight, rstd, grad, dx, partial, (int)rows, (int)d, e, s);
+  if (d > 2048)
+    rc = e ? rms_bwd_wide<true>(x, weight, rstd, grad, dx, partial, r, w, vec, s)
+           : rms_bwd_wide<false>(x, weight, rstd, grad, dx, partial, r, w, vec, s);
+  else if (!vec) rc = launch_rms_bwd<0>(x, weight, rstd, grad, dx, partial, r, w, e, s);
+  else if (segs <= 1) rc = launch_rms_bwd<1>(x, weight, rstd, grad, dx, partial, r, w, e, s);
+  else if (segs <= 2) rc = launch_rms_bwd<2>(x, weight, rstd, grad, dx, partial, r, w, e, s);
+  else rc = launch_rms_bwd<4>(x, weight, rstd, grad, dx, partial, r, w, e, s);
   if (rc) return rc;
-  const int groups = cdiv(rows, kRmsRowsPerBlock);
-  const bool vec = d % 4 == 0 && reinterpret_cast<unsigned long>(partial) % 16 == 0;
-  hipLaunchKernelGGL(vec ? rms_weight_reduce_kernel<true> : rms_weight_reduce_kernel<false>,
+  const int groups = cdiv(rows, rms_rows_per_block(rows, d));
+  const bool vec_reduce = d % 4 == 0 && reinterpret_cast<unsigned long>(partial) % 16 == 0;
+  hipLaunchKernelGGL(vec_reduce ? rms_weight_reduce_kernel<true> : rms_weight_reduce_kernel<false>,
                      dim3(cdiv(d, kRmsReduceCols)), dim3(256), 0, s, partial, dweight, groups,
                      (int)d, e);
   return hip_check(hipGetLastError(), "rmsnorm weight reduce launch");
@@ -133,7 +162,7 @@ extern "C" int ws_rmsnorm_backward(const void* x, const float* weight, const flo
 namespace {
 
 constexpr long kStaticPartialFloats = 1L << 20;  // 4 MiB: rows x d up to 2^25 at d % 8 == 0
-constexpr int kStaticMaxWidth = 4096;  // the widest row of a spill-free kernel (8 segments)
+constexpr int kStaticMaxWidth = 8192;  // the widest row any RMSNorm backward kernel takes
 __device__ __align__(256) float scratch[kStaticPartialFloats];
 
 constexpr int kScratchDevices = 64;
@@ -169,12 +198,12 @@ extern "C" int ws_rmsnorm_backward_static(const void* x, const float* weight, co
                                           void* stream) {
   if (rows < 1 || d < 1 || !fits_i32(rows) || !fits_i32(d))
     return set_error(kInvalid, "invalid RMSNorm shape");
-  // Rows wider than 4096 take the 16-segment kernel, which spills registers to private
-  // scratch memory that the HIP runtime would have to allocate.
+  // Checked here, before any device call (the row kernels take at most 8192 columns; none
+  // of them uses private scratch memory, which the HIP runtime would have to allocate).
   if (d > kStaticMaxWidth)
     return set_error(kInvalid,
                      "the allocation-free RMSNorm backward takes rows of at most %d columns "
-                     "(got %ld; use ws_rmsnorm_backward)",
+                     "(got %ld)",
                      kStaticMaxWidth, (long)d);
   const long need = ws_rmsnorm_backward_partial_floats(rows, d);
   if (need > kStaticPartialFloats)
