@@ -90,6 +90,15 @@ def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
     return wide.to(x.dtype) * weight.to(x.dtype)
 
 
+def rmsnorm_fp32_product(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """The BF16 RMSNorm kernel without eager rounding (ops/activation_execution.py:96-110,
+    ROUND = False: the compiled path): r(f32(x) rstd w), the product in FP32 and one BF16
+    rounding on the store."""
+    wide = x.float()
+    rstd = torch.rsqrt(wide.pow(2).mean(dim=-1, keepdim=True) + eps)
+    return (wide * rstd * weight.float()).to(x.dtype)
+
+
 def rmsnorm_gate_projection(x, norm_weight, eps, weight, gate):
     """RMSNorm -> in_proj -> sigmoid on the gate slice
     (warpstate/model.py:120-121, :109, :174): out = r(y @ W^T) with

@@ -539,6 +539,24 @@ def test_standalone_rmsnorm_forward_backward(shape):
     assert rel_l2(w.grad, w_ref.grad) <= 3e-3
 
 
+@pytest.mark.parametrize("shape", [(37, 64), (257, 2048), (40, 4096), (9, 8192), (33, 1001),
+                                   (5, 8200), (3, 20)])
+def test_standalone_rmsnorm_forward_without_eager_rounding(shape):
+    """The compiled-path forward (eager_rounding=False: r(x rstd w) with the product in FP32)
+    against the oracle, at widths of the register kernels (up to 8192), the two-pass vector
+    kernel (8200) and the scalar kernel (widths not a multiple of 8)."""
+    from ops.activation_execution import bf16_rmsnorm
+
+    gen = _gen(959)
+    weight = torch.rand(shape[-1], generator=gen) * 1.9 + 0.1
+    x = torch.randn(shape, generator=gen).bfloat16()
+    with torch.no_grad():
+        out, rstd = bf16_rmsnorm(x.cuda(), weight.cuda(), 1e-5, False)
+    torch.cuda.synchronize()
+    assert_bf16_close(out, oracle.rmsnorm_fp32_product(x, weight, 1e-5), "rmsnorm, FP32 product")
+    assert_f32_close(rstd.cpu(), oracle.rms_rstd(x.reshape(-1, shape[-1]), 1e-5), "rstd")
+
+
 @pytest.mark.parametrize("shape", [(3, 20), (5, 100), (33, 27), (9, 1001), (70, 4100),
                                    (2, 3, 8190)])
 def test_standalone_rmsnorm_backward_any_width(shape):

@@ -201,6 +201,27 @@ def test_rmsnorm_zero_row_and_scale_invariance():
     assert torch.allclose(ms[torch.arange(8) != 3], torch.ones(7), atol=1e-2)
 
 
+def test_rmsnorm_fp32_product_against_float64_and_special_cases():
+    """The compiled-path RMSNorm (no eager rounding) is the float64 closed form rounded once
+    to BF16: every element within one BF16 rounding of it. A zero row and a zero weight give
+    exact zeros; scaling a row by 4 (exact in BF16) leaves it unchanged when eps is
+    negligible; and it differs from the eager form, which rounds x rstd and w first."""
+    gen = torch.Generator().manual_seed(8)
+    x = torch.randn(16, 200, generator=gen).bfloat16()
+    x[5] = 0
+    nw = torch.randn(200, generator=gen) * 0.1 + 1
+    y = oracle.rmsnorm_fp32_product(x, nw, 1e-6)
+    x64 = x.double()
+    want = x64 * torch.rsqrt(x64.pow(2).mean(-1, keepdim=True) + 1e-6) * nw.double()
+    ulp = want.abs().clamp_min(1e-30) * 2.0 ** -8
+    assert bool(((y.double() - want).abs() <= ulp).all())
+    assert torch.count_nonzero(y[5]) == 0
+    assert torch.count_nonzero(oracle.rmsnorm_fp32_product(x, torch.zeros(200), 1e-6)) == 0
+    assert torch.equal(oracle.rmsnorm_fp32_product(x * 4, nw, 1e-12),
+                       oracle.rmsnorm_fp32_product(x, nw, 1e-12))
+    assert not torch.equal(y, oracle.rmsnorm(x, nw, 1e-6))
+
+
 # --- Residual epilogue ---------------------------------------------------------------
 
 def test_residual_fixture_and_zero_weight_identity():

@@ -22,31 +22,38 @@ static inline bool al(const void* p, int bytes) {
 }
 
 namespace ws {
-// y = r(r(x rstd) r(w)) and rstd for rows of x (row stride ldx) into a contiguous y: the
-// RMSNorm pass before the fused input projection, also the eager standalone RMSNorm
-// forward. Rows of at most 4096 vector-aligned features stay in registers (x read once).
+// y and rstd for rows of x (row stride ldx) into a contiguous y, with the eager rounding
+// y = r(r(x rstd) r(w)) or the FP32 product r(x rstd w): the RMSNorm pass before the fused
+// input projection (eager), also the standalone RMSNorm forward. Rows of at most 8192
+// vector-aligned features stay in registers (x read once).
+template <bool EAGER>
+static void rmsnorm_rows_eager(const unsigned short* xs, long ldx, const float* w,
+                               unsigned short* ys, float* rstd, long m, long k, float eps,
+                               int vec, hipStream_t s) {
+  const dim3 grid(cdiv(m, 4));
+  auto reg = [&](auto kernel) {
+    hipLaunchKernelGGL(kernel, grid, dim3(256), 0, s, xs, ldx, w, ys, rstd, (int)m, (int)k, eps);
+  };
+  if (vec && k <= 512) reg(rmsnorm_rows_reg_kernel<1, EAGER>);
+  else if (vec && k <= 1024) reg(rmsnorm_rows_reg_kernel<2, EAGER>);
+  else if (vec && k <= 2048) reg(rmsnorm_rows_reg_kernel<4, EAGER>);
+  else if (vec && k <= 4096) reg(rmsnorm_rows_reg_kernel<8, EAGER>);
+  else if (vec && k <= 8192) reg(rmsnorm_rows_reg_kernel<16, EAGER>);
+  else
+    hipLaunchKernelGGL(rmsnorm_rows_kernel<EAGER>, grid, dim3(256), 0, s, xs, ldx, w, ys, rstd,
+                       (int)m, (int)k, eps, vec);
+}
+
 int launch_rmsnorm_rows(const void* x, long ldx, const float* w, void* y, float* rstd, long m,
-                        long k, float eps, hipStream_t s) {
+                        long k, float eps, bool eager, hipStream_t s) {
   // The vector kernels read x and the FP32 weight, and write y, as 16-byte pieces.
   const int vec = (ldx % 8 == 0) && (k % 8 == 0) && al(x, 16) && al(y, 16) && al(w, 16);
-  const dim3 grid(cdiv(m, 4));
   const auto* xs = static_cast<const unsigned short*>(x);
   auto* ys = static_cast<unsigned short*>(y);
-  if (vec && k <= 512)
-    hipLaunchKernelGGL(rmsnorm_rows_reg_kernel<1>, grid, dim3(256), 0, s, xs, ldx, w, ys, rstd,
-                       (int)m, (int)k, eps);
-  else if (vec && k <= 1024)
-    hipLaunchKernelGGL(rmsnorm_rows_reg_kernel<2>, grid, dim3(256), 0, s, xs, ldx, w, ys, rstd,
-                       (int)m, (int)k, eps);
-  else if (vec && k <= 2048)
-    hipLaunchKernelGGL(rmsnorm_rows_reg_kernel<4>, grid, dim3(256), 0, s, xs, ldx, w, ys, rstd,
-                       (int)m, (int)k, eps);
-  else if (vec && k <= 4096)
-    hipLaunchKernelGGL(rmsnorm_rows_reg_kernel<8>, grid, dim3(256), 0, s, xs, ldx, w, ys, rstd,
-                       (int)m, (int)k, eps);
+  if (eager)
+    rmsnorm_rows_eager<true>(xs, ldx, w, ys, rstd, m, k, eps, vec, s);
   else
-    hipLaunchKernelGGL(rmsnorm_rows_kernel, grid, dim3(256), 0, s, xs, ldx, w, ys, rstd, (int)m,
-                       (int)k, eps, vec);
+    rmsnorm_rows_eager<false>(xs, ldx, w, ys, rstd, m, k, eps, vec, s);
   return hip_check(hipGetLastError(), "rmsnorm rows launch");
 }
 }  // namespace ws
@@ -64,7 +71,7 @@ extern "C" int ws_rmsnorm_gate_mm(const void* x, int64_t x_s0, const float* norm
   if (int rc = check_out_stride(n, 2, "output")) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
   // Prologue: one pass over x writes the normalized BF16 operand y and rstd.
-  if (int rc = launch_rmsnorm_rows(x, x_s0, norm_weight, normed, rstd, m, k, eps, s)) return rc;
+  if (int rc = launch_rmsnorm_rows(x, x_s0, norm_weight, normed, rstd, m, k, eps, true, s)) return rc;
   GemmParams p{};
   p.a = desc_a(normed, k, 1);
   p.b = desc_b(b, b_s0, b_s1);

@@ -8,10 +8,18 @@
 namespace ws {
 
 // ---------------------------------------------------------------------------------------
-// RMSNorm of x (row stride ldx) into a contiguous BF16 y with the eager rounding of
-// RMSNorm.forward (warpstate/model.py:25-28): y = r(r(x * rstd) * r(w)); also stores
-// rstd. One wave per row; with `vec`, 16-byte loads and stores of 8 elements per lane.
-// The GEMM prologue of the fused input projection.
+// RMSNorm of x (row stride ldx) into a contiguous BF16 y; also stores rstd
+// (warpstate/model.py:25-28, ops/activation_execution.py:96-110). EAGER is the eager
+// rounding of RMSNorm.forward, y = r(r(x * rstd) * r(w)); without it y = r(x * rstd * w)
+// with the product in FP32 (the compiled path). One wave per row; with `vec`, 16-byte loads
+// and stores of 8 elements per lane. EAGER is a template argument: tested at run time, the
+// compiler computes every element both ways and selects.
+template <bool EAGER>
+__device__ __forceinline__ float rms_out(float xv, float r, float wv) {
+  return EAGER ? rbf16(xv * r) * rbf16(wv) : (xv * r) * wv;
+}
+
+template <bool EAGER>
 static __global__ void __launch_bounds__(256) rmsnorm_rows_kernel(
     const unsigned short* __restrict__ x, long ldx, const float* __restrict__ w,
     unsigned short* __restrict__ y, float* __restrict__ rstd, int rows, int D, float eps,
@@ -48,17 +56,14 @@ static __global__ void __launch_bounds__(256) rmsnorm_rows_kernel(
       const float wv[8] = {w0[0], w0[1], w0[2], w0[3], w1[0], w1[1], w1[2], w1[3]};
       u32x4_t o;
 #pragma unroll
-      for (int d = 0; d < 4; ++d) {
-        const float z0 = rbf16(lo_bf16(v[d]) * r), z1 = rbf16(hi_bf16(v[d]) * r);
-        o[d] = pack_bf16x2(z0 * rbf16(wv[2 * d]), z1 * rbf16(wv[2 * d + 1]));
-      }
+      for (int d = 0; d < 4; ++d)
+        o[d] = pack_bf16x2(rms_out<EAGER>(lo_bf16(v[d]), r, wv[2 * d]),
+                           rms_out<EAGER>(hi_bf16(v[d]), r, wv[2 * d + 1]));
       *reinterpret_cast<u32x4_t*>(yr + c) = o;
     }
   } else {
-    for (int c = lane; c < D; c += 64) {
-      const float z = rbf16(bf16_bits_to_f32(xr[c]) * r);
-      yr[c] = to_bf16_bits(z * rbf16(w[c]));
-    }
+    for (int c = lane; c < D; c += 64)
+      yr[c] = to_bf16_bits(rms_out<EAGER>(bf16_bits_to_f32(xr[c]), r, w[c]));
   }
   if (lane == 0) rstd[row] = r;
 }
@@ -66,7 +71,7 @@ static __global__ void __launch_bounds__(256) rmsnorm_rows_kernel(
 // rmsnorm_rows_kernel for vector rows of at most 512 NC elements: each lane keeps its NC
 // 16-byte chunks of the row in registers (all loads in flight at once), so x is read
 // once. Same sums in the same order, so the same bits as rmsnorm_rows_kernel.
-template <int NC>
+template <int NC, bool EAGER>
 static __global__ void __launch_bounds__(256) rmsnorm_rows_reg_kernel(
     const unsigned short* __restrict__ x, long ldx, const float* __restrict__ w,
     unsigned short* __restrict__ y, float* __restrict__ rstd, int rows, int D, float eps) {
@@ -101,41 +106,10 @@ static __global__ void __launch_bounds__(256) rmsnorm_rows_reg_kernel(
     const float wv[8] = {w0[0], w0[1], w0[2], w0[3], w1[0], w1[1], w1[2], w1[3]};
     u32x4_t o;
 #pragma unroll
-    for (int d = 0; d < 4; ++d) {
-      const float z0 = rbf16(lo_bf16(v[i][d]) * r), z1 = rbf16(hi_bf16(v[i][d]) * r);
-      o[d] = pack_bf16x2(z0 * rbf16(wv[2 * d]), z1 * rbf16(wv[2 * d + 1]));
-    }
+    for (int d = 0; d < 4; ++d)
+      o[d] = pack_bf16x2(rms_out<EAGER>(lo_bf16(v[i][d]), r, wv[2 * d]),
+                         rms_out<EAGER>(hi_bf16(v[i][d]), r, wv[2 * d + 1]));
     *reinterpret_cast<u32x4_t*>(yr + c) = o;
-  }
-  if (lane == 0) rstd[row] = r;
-}
-
-// Standalone BF16 RMSNorm forward (ops/activation_execution.py:96-110): z = x * rstd,
-// y = z * w with z and w rounded to BF16 when eager; also stores rstd.
-static __global__ void __launch_bounds__(256) rmsnorm_fwd_kernel(const unsigned short* __restrict__ x,
-                                                          const float* __restrict__ w,
-                                                          unsigned short* __restrict__ y,
-                                                          float* __restrict__ rstd, int rows,
-                                                          int D, float eps, int eager) {
-  const int lane = threadIdx.x & 63;
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= rows) return;
-  const unsigned short* xr = x + (long)row * D;
-  float acc = 0.0f;
-  for (int c = lane; c < D; c += 64) {
-    float a = bf16_bits_to_f32(xr[c]);
-    acc += a * a;
-  }
-  acc = wave_sum(acc);
-  const float r = 1.0f / sqrtf(acc / (float)D + eps);
-  for (int c = lane; c < D; c += 64) {
-    float z = bf16_bits_to_f32(xr[c]) * r;
-    float wc = w[c];
-    if (eager) {
-      z = rbf16(z);
-      wc = rbf16(wc);
-    }
-    y[(long)row * D + c] = to_bf16_bits(z * wc);
   }
   if (lane == 0) rstd[row] = r;
 }

@@ -7,7 +7,7 @@
 
 namespace ws {
 int launch_rmsnorm_rows(const void* x, long ldx, const float* w, void* y, float* rstd, long m,
-                        long k, float eps, hipStream_t s);
+                        long k, float eps, bool eager, hipStream_t s);
 }
 
 using namespace ws;
@@ -43,15 +43,9 @@ extern "C" int ws_rmsnorm_forward(const void* x, const float* weight, void* y, f
   if (!x || !weight || !y || !rstd) return set_error(kInvalid, "null pointer");
   if (rows < 0 || d < 1 || !fits_i32(rows) || !fits_i32(d)) return set_error(kInvalid, "invalid RMSNorm shape");
   if (rows == 0) return kOk;
-  // Eager rounding is the arithmetic of the fused projection's row pass: same kernel.
-  if (eager_rounding)
-    return launch_rmsnorm_rows(x, d, weight, y, rstd, rows, d, eps,
-                               static_cast<hipStream_t>(stream));
-  hipLaunchKernelGGL(rmsnorm_fwd_kernel, dim3(cdiv(rows, 4)), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), static_cast<const unsigned short*>(x), weight,
-                     static_cast<unsigned short*>(y), rstd, (int)rows, (int)d, eps,
-                     eager_rounding ? 1 : 0);
-  return hip_check(hipGetLastError(), "rmsnorm forward launch");
+  // The kernels of the fused projection's row pass (eager rounding), in either mode.
+  return launch_rmsnorm_rows(x, d, weight, y, rstd, rows, d, eps, eager_rounding != 0,
+                             static_cast<hipStream_t>(stream));
 }
 
 // Rows per block of the RMSNorm backward: 32 for rows of up to 2048 columns (4 waves, one
