@@ -17,9 +17,6 @@ static inline OperandDesc desc_a(const void* a, long s0, long s1) {
 static inline OperandDesc desc_b(const void* b, long s0, long s1) {
   return OperandDesc{static_cast<const unsigned short*>(b), s1, s0};
 }
-static inline bool al(const void* p, int bytes) {
-  return reinterpret_cast<unsigned long>(p) % bytes == 0;
-}
 
 namespace ws {
 // y and rstd for rows of x (row stride ldx) into a contiguous y, with the eager rounding

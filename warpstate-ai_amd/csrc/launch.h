@@ -15,6 +15,9 @@ int set_error(int code, const char* fmt, ...);  // records the thread's last err
 int device_cus();                               // compute units of the current device
 int ensure_lds(const void* kernel, int bytes);  // raises the kernel's dynamic LDS limit on this device to >= bytes
 
+// Whether a pointer is aligned to `bytes`.
+inline bool al(const void* p, int bytes) { return reinterpret_cast<unsigned long>(p) % bytes == 0; }
+
 inline int hip_check(hipError_t e, const char* what) {
   if (e != hipSuccess) return set_error(kHipError, "%s: %s", what, hipGetErrorString(e));
   return kOk;

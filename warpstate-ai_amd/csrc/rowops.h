@@ -533,6 +533,69 @@ static __global__ void __launch_bounds__(256) swiglu_bwd_kernel(const unsigned s
   dx[p + H] = to_bf16_bits(dgate);
 }
 
+// The two standalone SwiGLU kernels above with 8 consecutive columns per thread (16-byte
+// loads and stores; H % 8 == 0 and 16-byte aligned buffers): the same arithmetic per
+// element, so the same bits.
+template <bool EAGER>
+static __global__ void __launch_bounds__(256) swiglu_fwd_vec_kernel(const unsigned short* __restrict__ packed,
+                                                             unsigned short* __restrict__ out,
+                                                             long chunks, int H) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= chunks) return;
+  const int per_row = H / 8;
+  const long row = i / per_row;
+  const int c = 8 * (int)(i - row * per_row);
+  const unsigned short* pr = packed + row * 2 * H + c;
+  const u32x4_t up = *reinterpret_cast<const u32x4_t*>(pr);
+  const u32x4_t gate = *reinterpret_cast<const u32x4_t*>(pr + H);
+  u32x4_t o;
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    float s0 = silu(lo_bf16(gate[d])), s1 = silu(hi_bf16(gate[d]));
+    if (EAGER) { s0 = rbf16(s0); s1 = rbf16(s1); }
+    o[d] = pack_bf16x2(s0 * lo_bf16(up[d]), s1 * hi_bf16(up[d]));
+  }
+  *reinterpret_cast<u32x4_t*>(out + row * H + c) = o;
+}
+
+template <bool EAGER>
+static __global__ void __launch_bounds__(256) swiglu_bwd_vec_kernel(const unsigned short* __restrict__ packed,
+                                                             const unsigned short* __restrict__ dyv,
+                                                             unsigned short* __restrict__ dx,
+                                                             long chunks, int H) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= chunks) return;
+  const int per_row = H / 8;
+  const long row = i / per_row;
+  const int c = 8 * (int)(i - row * per_row);
+  const long p = row * 2 * H + c;
+  const u32x4_t up = *reinterpret_cast<const u32x4_t*>(packed + p);
+  const u32x4_t gate = *reinterpret_cast<const u32x4_t*>(packed + p + H);
+  const u32x4_t dyw = *reinterpret_cast<const u32x4_t*>(dyv + row * H + c);
+  u32x4_t du, dg;
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    float r_up[2], r_dg[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const float u = h ? hi_bf16(up[d]) : lo_bf16(up[d]);
+      const float g = h ? hi_bf16(gate[d]) : lo_bf16(gate[d]);
+      const float y = h ? hi_bf16(dyw[d]) : lo_bf16(dyw[d]);
+      const float sg = sigmoid(g);
+      float sl = g * sg;
+      if (EAGER) sl = rbf16(sl);
+      float dsilu = y * u;
+      if (EAGER) dsilu = rbf16(dsilu);
+      r_up[h] = y * sl;
+      r_dg[h] = (dsilu * sg) * (1.0f + g * (1.0f - sg));
+    }
+    du[d] = pack_bf16x2(r_up[0], r_up[1]);
+    dg[d] = pack_bf16x2(r_dg[0], r_dg[1]);
+  }
+  *reinterpret_cast<u32x4_t*>(dx + p) = du;
+  *reinterpret_cast<u32x4_t*>(dx + p + H) = dg;
+}
+
 // ---------------------------------------------------------------------------------------
 // Cross-entropy, pass 1 combine: lse[r] = M + log(sum_p s_p e^(m_p - M)) over the
 // per-(row, column block) partials; loss[r] = lse - logit[target] for targets != -100,

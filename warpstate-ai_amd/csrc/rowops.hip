@@ -18,6 +18,18 @@ extern "C" int ws_swiglu_forward(const void* packed, void* out, int64_t rows, in
   if (rows < 0 || h < 1 || !fits_i32(h)) return set_error(kInvalid, "invalid SwiGLU shape");
   const long total = rows * h;
   if (total == 0) return kOk;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (h % 8 == 0 && al(packed, 16) && al(out, 16)) {
+    const long chunks = total / 8;
+    const dim3 grid((unsigned)((chunks + 255) / 256));
+    const auto* pk = static_cast<const unsigned short*>(packed);
+    auto* o = static_cast<unsigned short*>(out);
+    if (eager_rounding)
+      hipLaunchKernelGGL(swiglu_fwd_vec_kernel<true>, grid, dim3(256), 0, s, pk, o, chunks, (int)h);
+    else
+      hipLaunchKernelGGL(swiglu_fwd_vec_kernel<false>, grid, dim3(256), 0, s, pk, o, chunks, (int)h);
+    return hip_check(hipGetLastError(), "swiglu forward launch");
+  }
   hipLaunchKernelGGL(swiglu_fwd_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
                      static_cast<hipStream_t>(stream), static_cast<const unsigned short*>(packed),
                      static_cast<unsigned short*>(out), total, (int)h, eager_rounding ? 1 : 0);
@@ -30,6 +42,19 @@ extern "C" int ws_swiglu_backward(const void* packed, const void* grad, void* ou
   if (rows < 0 || h < 1 || !fits_i32(h)) return set_error(kInvalid, "invalid SwiGLU shape");
   const long total = rows * h;
   if (total == 0) return kOk;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (h % 8 == 0 && al(packed, 16) && al(grad, 16) && al(out, 16)) {
+    const long chunks = total / 8;
+    const dim3 grid((unsigned)((chunks + 255) / 256));
+    const auto* pk = static_cast<const unsigned short*>(packed);
+    const auto* g = static_cast<const unsigned short*>(grad);
+    auto* o = static_cast<unsigned short*>(out);
+    if (eager_rounding)
+      hipLaunchKernelGGL(swiglu_bwd_vec_kernel<true>, grid, dim3(256), 0, s, pk, g, o, chunks, (int)h);
+    else
+      hipLaunchKernelGGL(swiglu_bwd_vec_kernel<false>, grid, dim3(256), 0, s, pk, g, o, chunks, (int)h);
+    return hip_check(hipGetLastError(), "swiglu backward launch");
+  }
   hipLaunchKernelGGL(swiglu_bwd_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
                      static_cast<hipStream_t>(stream), static_cast<const unsigned short*>(packed),
                      static_cast<const unsigned short*>(grad), static_cast<unsigned short*>(out),
