@@ -304,7 +304,7 @@ def bench_gpu(args):
     hbm = {"rmsnorm_rows": {"ms": round(rows_ms, 4), "bytes": rows_bytes,
                             "gbs": round(rows_bytes / rows_ms / 1e6, 1),
                             "frac_hbm": round(rows_bytes / rows_ms / 1e6 / PEAK_HBM_GBS, 4),
-                            "kernel": "rmsnorm_rows_reg_kernel<4> (qkv_fwd row pass)"}}
+                            "kernel": "rmsnorm_rows_reg_kernel<4, true> (qkv_fwd row pass)"}}
     # RMSNorm backward of the step (dX and the weight gradient, both launches): x and the
     # incoming gradient read, dX written, rstd read and the FP32 weight gradient written
     # once each (the per-block partials are not counted).
