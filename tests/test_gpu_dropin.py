@@ -350,15 +350,19 @@ def _fused_adapter_case(size, hip_calls):
         assert logits.shape == (*tokens, vocab)
 
 
+@pytest.mark.parametrize("dims", [(256, 512, 2048), (100, 250, 1030)],
+                         ids=["d256", "d100_ffn250_vocab1030"])
 @pytest.mark.parametrize("variant", ["eager", "checkpointed", "compiled_cores", "compiled_model"])
-def test_fused_adapter_on_the_reference_core_layout(variant, hip_calls):
+def test_fused_adapter_on_the_reference_core_layout(variant, dims, hip_calls):
     """A model in the reference's own layout (one WarpStateCore.forward with _split, the
     inline gate sigmoid and residual adds, and the inline chunked loss; no seams): the
     adapter attaches its RMSNorm, Linear and SwiGLU modules and the loss (through a forward
     wrap that stops at final_norm), and loss and every parameter gradient agree with the
     unpatched model at the reference's bars (loss rtol 1e-3, gradient cosine > 0.999)
     under BF16 autocast with BF16 residuals. No weight gradient is formed in a cleared
-    buffer: every one comes from the FP32 store GEMMs, through autograd."""
+    buffer: every one comes from the FP32 store GEMMs, through autograd. The second width
+    set (model width 100, hidden 250, vocabulary 1030: none a multiple of 8) takes the
+    library's generic loaders and row kernels throughout."""
     from inline_layout_model import InlineLM
     from warpstate.config import WarpStateConfig
 
@@ -367,10 +371,11 @@ def test_fused_adapter_on_the_reference_core_layout(variant, hip_calls):
 
     try:
         torch.manual_seed(733)
-        vocab, tokens = 2048, (4, 64)
+        d_model, ffn, vocab = dims
+        tokens = (4, 64)
         reference = InlineLM(WarpStateConfig(
-            vocab_size=vocab, d_model=256, n_heads=4, n_cores=2, logical_depth=3,
-            ffn_hidden=512, loss_chunk_size=96,
+            vocab_size=vocab, d_model=d_model, n_heads=4, n_cores=2, logical_depth=3,
+            ffn_hidden=ffn, loss_chunk_size=96,
             gradient_checkpointing=variant == "checkpointed")).train().cuda()
         actual = copy.deepcopy(reference)
         keys = tuple(actual.state_dict())
