@@ -102,9 +102,13 @@ def test_exact_small_integer_products():
 
 
 @pytest.mark.parametrize("shape,stride_pad", [((64, 64), 0), ((1000, 2056), 8), ((37, 91), 5),
-                                              ((2048, 11264), 0)])
+                                              ((2048, 11264), 0), ((8, 8), 0), ((24, 520), 16),
+                                              ((11264, 2048), 0), ((9216, 2048), 0),
+                                              ((2048, 5632), 8), ((40, 12), 4)])
 def test_transpose_is_bit_exact(shape, stride_pad):
-    """The weight-layout transpose used by the input-gradient GEMMs moves bits only."""
+    """The weight-layout transpose used by the input-gradient GEMMs moves bits only: the
+    register kernel (rows, columns and stride multiples of 8, including partial 64 x 256
+    tiles) and the LDS kernel (any other shape)."""
     from ops.fused_execution import transpose
 
     rows, cols = shape

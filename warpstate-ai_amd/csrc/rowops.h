@@ -867,51 +867,54 @@ static __global__ void __launch_bounds__(256) splitk_bf16_kernel(const float* __
 namespace ws {
 
 // BF16 transpose out[c, r] = in[r, c] of a [rows, cols] matrix with row stride ld_in into a
-// contiguous [cols, rows] result. 64 x 64 tiles through LDS (rows padded by 8 elements so
-// the column reads do not collide); 16-byte global loads and stores when rows, cols and
-// ld_in are multiples of 8 and both pointers are 16-byte aligned. HBM-bound.
+// contiguous [cols, rows] result, for any shape: 64 x 64 tiles through LDS (rows padded by 8
+// elements so the column reads do not collide), one element per access. Shapes whose rows,
+// columns and stride are multiples of 8 take transpose_bf16_reg_kernel below. HBM-bound.
 static __global__ void __launch_bounds__(256) transpose_bf16_kernel(
     const unsigned short* __restrict__ in, long ld_in, unsigned short* __restrict__ out,
-    int rows, int cols, int vec) {
+    int rows, int cols) {
   __shared__ unsigned short tile[64][72];
   const int r0 = blockIdx.y * 64, c0 = blockIdx.x * 64;
   const int t = threadIdx.x;
-  if (vec) {
-    // 64 rows x 8 chunks of 8 columns: two chunks per thread.
+  for (int idx = t; idx < 64 * 64; idx += 256) {
+    const int r = idx >> 6, c = idx & 63;
+    tile[r][c] = (r0 + r < rows && c0 + c < cols) ? in[(long)(r0 + r) * ld_in + c0 + c] : 0;
+  }
+  __syncthreads();
+  for (int idx = t; idx < 64 * 64; idx += 256) {
+    const int c = idx >> 6, r = idx & 63;
+    if (c0 + c < cols && r0 + r < rows) out[(long)(c0 + c) * rows + r0 + r] = tile[r][c];
+  }
+}
+
+// The transpose held in registers (rows, cols and ld_in multiples of 8, both pointers
+// 16-byte aligned): each lane moves one 8 x 8 block, read as eight 16-byte row pieces and
+// written as eight 16-byte column pieces after an in-register transpose (one byte
+// permutation per output word). The 64 lanes of a wave cover a 64 x 64 tile (lane
+// 8 * br + bc holds block (br, bc)), so every load instruction reads, and every store
+// writes, eight whole 128-byte lines. No LDS and no barrier. Streaming (non-temporal)
+// stores: 5.5 -> 6.0-6.4 TB/s on the weight shapes of the layer step.
+static __global__ void __launch_bounds__(256) transpose_bf16_reg_kernel(
+    const unsigned short* __restrict__ in, long ld_in, unsigned short* __restrict__ out,
+    int rows, int cols) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = blockIdx.y * 64 + 8 * (lane >> 3);
+  const int c = (blockIdx.x * 4 + wave) * 64 + 8 * (lane & 7);
+  if (r >= rows || c >= cols) return;  // whole blocks: rows and cols are multiples of 8
+  u32x4_t w[8];
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      const int idx = t + 256 * q, r = idx >> 3, ch = idx & 7;
-      u32x4_t v = {0u, 0u, 0u, 0u};
-      if (r0 + r < rows && c0 + 8 * ch < cols)
-        v = *reinterpret_cast<const u32x4_t*>(in + (long)(r0 + r) * ld_in + c0 + 8 * ch);
+  for (int j = 0; j < 8; ++j)
+    w[j] = *reinterpret_cast<const u32x4_t*>(in + (long)(r + j) * ld_in + c);
 #pragma unroll
-      for (int d = 0; d < 4; ++d) {
-        tile[r][8 * ch + 2 * d] = (unsigned short)(v[d] & 0xffffu);
-        tile[r][8 * ch + 2 * d + 1] = (unsigned short)(v[d] >> 16);
-      }
-    }
-    __syncthreads();
+  for (int q = 0; q < 8; ++q) {
+    // Output row c + q: column q of the block, from word q / 2 of each input row (low half
+    // for even q), rows 2p and 2p + 1 packed into word p.
+    u32x4_t o;
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      const int idx = t + 256 * q, c = idx >> 3, ch = idx & 7;
-      if (c0 + c < cols && r0 + 8 * ch < rows) {
-        u32x4_t v;
-#pragma unroll
-        for (int d = 0; d < 4; ++d)
-          v[d] = (unsigned)tile[8 * ch + 2 * d][c] | ((unsigned)tile[8 * ch + 2 * d + 1][c] << 16);
-        *reinterpret_cast<u32x4_t*>(out + (long)(c0 + c) * rows + r0 + 8 * ch) = v;
-      }
-    }
-  } else {
-    for (int idx = t; idx < 64 * 64; idx += 256) {
-      const int r = idx >> 6, c = idx & 63;
-      tile[r][c] = (r0 + r < rows && c0 + c < cols) ? in[(long)(r0 + r) * ld_in + c0 + c] : 0;
-    }
-    __syncthreads();
-    for (int idx = t; idx < 64 * 64; idx += 256) {
-      const int c = idx >> 6, r = idx & 63;
-      if (c0 + c < cols && r0 + r < rows) out[(long)(c0 + c) * rows + r0 + r] = tile[r][c];
-    }
+    for (int p = 0; p < 4; ++p)
+      o[p] = __builtin_amdgcn_perm(w[2 * p + 1][q >> 1], w[2 * p][q >> 1],
+                                   (q & 1) ? 0x07060302u : 0x05040100u);
+    __builtin_nontemporal_store(o, reinterpret_cast<u32x4_t*>(out + (long)(c + q) * rows + r));
   }
 }
 

@@ -243,9 +243,15 @@ extern "C" int ws_transpose_bf16(const void* in, int64_t ld_in, void* out, int64
     return set_error(kInvalid, "invalid transpose shape");
   const unsigned long pi = reinterpret_cast<unsigned long>(in), po = reinterpret_cast<unsigned long>(out);
   const int vec = rows % 8 == 0 && cols % 8 == 0 && ld_in % 8 == 0 && pi % 16 == 0 && po % 16 == 0;
+  if (vec) {
+    hipLaunchKernelGGL(transpose_bf16_reg_kernel, dim3(cdiv(cols, 256), cdiv(rows, 64)), dim3(256),
+                       0, static_cast<hipStream_t>(stream), static_cast<const unsigned short*>(in),
+                       (long)ld_in, static_cast<unsigned short*>(out), (int)rows, (int)cols);
+    return hip_check(hipGetLastError(), "transpose launch");
+  }
   hipLaunchKernelGGL(transpose_bf16_kernel, dim3(cdiv(cols, 64), cdiv(rows, 64)), dim3(256), 0,
                      static_cast<hipStream_t>(stream), static_cast<const unsigned short*>(in),
-                     (long)ld_in, static_cast<unsigned short*>(out), (int)rows, (int)cols, vec);
+                     (long)ld_in, static_cast<unsigned short*>(out), (int)rows, (int)cols);
   return hip_check(hipGetLastError(), "transpose launch");
 }
 
