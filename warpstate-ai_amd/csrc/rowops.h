@@ -119,71 +119,98 @@ static __global__ void __launch_bounds__(256) rmsnorm_rows_reg_kernel(
 // and the weight-gradient partial sum over this block's rows of r?(dy z) (r? = BF16
 // rounding when eager). Rows of up to 2048 columns: one wave per row, 16-byte loads: lane
 // l owns columns 8 l + 512 s (s < SEGS), and keeps its x and dy chunks in registers between
-// the two passes over the row. A block of 4 waves takes kRmsRowsPerBlock consecutive rows
-// and writes one partial weight-gradient row (summed across its waves in LDS). Wider rows
-// take the block-per-row kernels below.
+// the two passes over the row. A block of kRmsWaves waves takes kRmsRowsPerBlock
+// consecutive rows (wave w the rows w, w + kRmsWaves, ...); each wave's weight-gradient
+// partial builds up in its own LDS row, and the waves' rows are added in wave order into
+// one partial row per block. Wider rows take the block-per-row kernels below.
 constexpr int kRmsRowsPerBlock = 32;
+constexpr int kRmsWaves = 8;
 
-// EAGER (the rounding mode) is a template argument: tested at run time, the compiler computes
-// every element both ways and selects.
+// The block's partial row: the waves' LDS rows added in wave order.
+__device__ __forceinline__ void rms_block_partial(const float* lds_part, float* dw_part, int D) {
+  __syncthreads();
+  for (int c = threadIdx.x; c < D; c += blockDim.x) {
+    float v = lds_part[c];
+#pragma unroll
+    for (int q = 1; q < kRmsWaves; ++q) v += lds_part[q * D + c];
+    dw_part[(long)blockIdx.x * D + c] = v;
+  }
+}
+
+// The partials and the (rounded) weight stay in LDS, not registers, so that the kernel fits
+// 128 VGPRs without spills: four waves per SIMD (two blocks per CU) keep twice the rows in
+// flight of a 4-wave block holding them in registers. EAGER (the rounding mode) is a
+// template argument: tested at run time, the compiler computes every element both ways and
+// selects.
 template <int SEGS, bool EAGER>
-static __global__ void __launch_bounds__(256) rmsnorm_bwd_kernel(
-    const unsigned short* __restrict__ x, const float* __restrict__ w,
-    const float* __restrict__ rstd, const unsigned short* __restrict__ dy,
-    unsigned short* __restrict__ dx, float* __restrict__ dw_part, int rows, int D) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  float wb[SEGS][8];
+static __global__ void __launch_bounds__(64 * kRmsWaves) __attribute__((amdgpu_waves_per_eu(4)))
+rmsnorm_bwd_kernel(const unsigned short* __restrict__ x, const float* __restrict__ w,
+                   const float* __restrict__ rstd, const unsigned short* __restrict__ dy,
+                   unsigned short* __restrict__ dx, float* __restrict__ dw_part, int rows, int D) {
+  extern __shared__ float lds_part[];  // [kRmsWaves][D] partials, then [D] weight
+  // The wave index as a scalar, so that row addresses are scalar bases plus one lane offset.
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  float* mine = lds_part + wave * D;
+  float* wl = lds_part + kRmsWaves * D;
+  for (int c = threadIdx.x; c < D; c += blockDim.x) wl[c] = EAGER ? rbf16(w[c]) : w[c];
 #pragma unroll
   for (int s = 0; s < SEGS; ++s) {
     const int c = 8 * lane + 512 * s;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float v = c + e < D ? w[c + e] : 0.0f;
-      wb[s][e] = EAGER ? rbf16(v) : v;
+    if (c < D) {
+      *reinterpret_cast<f32x4_t*>(mine + c) = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      *reinterpret_cast<f32x4_t*>(mine + c + 4) = f32x4_t{0.f, 0.f, 0.f, 0.f};
     }
   }
-  float part[SEGS][8];
-#pragma unroll
-  for (int s = 0; s < SEGS; ++s)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) part[s][e] = 0.0f;
+  __syncthreads();
 
   const int row_end = min(rows, (blockIdx.x + 1) * kRmsRowsPerBlock);
   // One row ahead: the next row's x and dy are requested before this row's reduction.
+  // (row is wave-uniform: the row bases are scalar and each lane adds its column offset.)
   auto load = [&](int row, u32x4_t (&xv)[SEGS], u32x4_t (&gv)[SEGS]) {
+    const unsigned short* xr = x + (long)row * D;
+    const unsigned short* gr = dy + (long)row * D;
 #pragma unroll
     for (int s = 0; s < SEGS; ++s) {
       const int c = 8 * lane + 512 * s;
       const bool ok = c < D && row < row_end;
-      xv[s] = ok ? *reinterpret_cast<const u32x4_t*>(x + (long)row * D + c) : u32x4_t{0u, 0u, 0u, 0u};
-      gv[s] = ok ? *reinterpret_cast<const u32x4_t*>(dy + (long)row * D + c) : u32x4_t{0u, 0u, 0u, 0u};
+      xv[s] = ok ? *reinterpret_cast<const u32x4_t*>(xr + c) : u32x4_t{0u, 0u, 0u, 0u};
+      gv[s] = ok ? *reinterpret_cast<const u32x4_t*>(gr + c) : u32x4_t{0u, 0u, 0u, 0u};
+    }
+  };
+  // dz = dy * w (rounded when EAGER) for the 8 columns of segment s, evaluated in both
+  // passes; columns past D read weight 0 (their dy is 0 too).
+  auto dz8 = [&](const u32x4_t& g, int s, float (&dz)[8]) {
+    const int c = 8 * lane + 512 * s;
+    f32x4_t w0 = {0.f, 0.f, 0.f, 0.f}, w1 = {0.f, 0.f, 0.f, 0.f};
+    if (c < D) {
+      w0 = *reinterpret_cast<const f32x4_t*>(wl + c);
+      w1 = *reinterpret_cast<const f32x4_t*>(wl + c + 4);
+    }
+    const float wv[8] = {w0[0], w0[1], w0[2], w0[3], w1[0], w1[1], w1[2], w1[3]};
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      dz[2 * d] = lo_bf16(g[d]) * wv[2 * d];
+      dz[2 * d + 1] = hi_bf16(g[d]) * wv[2 * d + 1];
+      if (EAGER) { dz[2 * d] = rbf16(dz[2 * d]); dz[2 * d + 1] = rbf16(dz[2 * d + 1]); }
     }
   };
   u32x4_t xn[SEGS], gn[SEGS];
   load(blockIdx.x * kRmsRowsPerBlock + wave, xn, gn);
-  for (int row = blockIdx.x * kRmsRowsPerBlock + wave; row < row_end; row += 4) {
+  for (int row = blockIdx.x * kRmsRowsPerBlock + wave; row < row_end; row += kRmsWaves) {
     const float r = rstd[row];
     u32x4_t xv[SEGS], gv[SEGS];
 #pragma unroll
     for (int s = 0; s < SEGS; ++s) { xv[s] = xn[s]; gv[s] = gn[s]; }
-    load(row + 4, xn, gn);
+    load(row + kRmsWaves, xn, gn);
     float dr = 0.0f;
-    // dy * w (rounded when EAGER), kept for the second pass up to 4096 columns (wider rows
-    // recompute it: their registers are spent on the row itself).
-    constexpr bool kKeep = SEGS <= 8;
-    float dz[kKeep ? SEGS : 1][8];
 #pragma unroll
     for (int s = 0; s < SEGS; ++s) {
+      float dz[8];
+      dz8(gv[s], s, dz);
 #pragma unroll
       for (int d = 0; d < 4; ++d) {
-        float dz0 = lo_bf16(gv[s][d]) * wb[s][2 * d], dz1 = hi_bf16(gv[s][d]) * wb[s][2 * d + 1];
-        if (EAGER) { dz0 = rbf16(dz0); dz1 = rbf16(dz1); }
-        if constexpr (kKeep) {
-          dz[s][2 * d] = dz0;
-          dz[s][2 * d + 1] = dz1;
-        }
-        dr += dz0 * lo_bf16(xv[s][d]);
-        dr += dz1 * hi_bf16(xv[s][d]);
+        dr += dz[2 * d] * lo_bf16(xv[s][d]);
+        dr += dz[2 * d + 1] * hi_bf16(xv[s][d]);
       }
     }
     dr = wave_sum(dr);
@@ -191,6 +218,11 @@ static __global__ void __launch_bounds__(256) rmsnorm_bwd_kernel(
 #pragma unroll
     for (int s = 0; s < SEGS; ++s) {
       const int c = 8 * lane + 512 * s;
+      if (c >= D) continue;
+      float dz[8];
+      dz8(gv[s], s, dz);
+      f32x4_t p0 = *reinterpret_cast<const f32x4_t*>(mine + c);
+      f32x4_t p1 = *reinterpret_cast<const f32x4_t*>(mine + c + 4);
       u32x4_t o;
 #pragma unroll
       for (int d = 0; d < 4; ++d) {
@@ -199,58 +231,44 @@ static __global__ void __launch_bounds__(256) rmsnorm_bwd_kernel(
         for (int h = 0; h < 2; ++h) {
           const float xs = h ? hi_bf16(xv[s][d]) : lo_bf16(xv[s][d]);
           const float gs = h ? hi_bf16(gv[s][d]) : lo_bf16(gv[s][d]);
-          float dzh;
-          if constexpr (kKeep) {
-            dzh = dz[s][2 * d + h];
-          } else {
-            dzh = gs * wb[s][2 * d + h];
-            if (EAGER) dzh = rbf16(dzh);
-          }
-          v2[h] = dzh * r + dsq * (2.0f * xs);
+          v2[h] = dz[2 * d + h] * r + dsq * (2.0f * xs);
           float z = xs * r;
           if (EAGER) z = rbf16(z);
           float pv = gs * z;
           if (EAGER) pv = rbf16(pv);
-          part[s][2 * d + h] += pv;
+          const int e = 2 * d + h;
+          if (e < 4) p0[e] += pv;
+          else p1[e - 4] += pv;
         }
         o[d] = pack_bf16x2(v2[0], v2[1]);
       }
-      if (c < D) *reinterpret_cast<u32x4_t*>(dx + (long)row * D + c) = o;
+      *reinterpret_cast<f32x4_t*>(mine + c) = p0;
+      *reinterpret_cast<f32x4_t*>(mine + c + 4) = p1;
+      *reinterpret_cast<u32x4_t*>(dx + (long)row * D + c) = o;
+      // One segment's LDS reads at a time: hoisting the next segments' reads would take
+      // registers past the 128 of four waves per SIMD.
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
-  // Sum the four waves' partials in LDS, then one row per block.
-  extern __shared__ float lds_part[];  // [4][D]
-#pragma unroll
-  for (int s = 0; s < SEGS; ++s) {
-    const int c = 8 * lane + 512 * s;
-    if (c < D) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) lds_part[wave * D + c + e] = part[s][e];
-    }
-  }
-  __syncthreads();
-  for (int c = threadIdx.x; c < D; c += blockDim.x)
-    dw_part[(long)blockIdx.x * D + c] =
-        ((lds_part[c] + lds_part[D + c]) + lds_part[2 * D + c]) + lds_part[3 * D + c];
+  rms_block_partial(lds_part, dw_part, D);
 }
 
 // The same RMSNorm backward for rows of up to 2048 columns with any width and alignment
-// (rows whose width is not a multiple of 8, views at odd offsets): lanes take columns lane, lane + 64,
-// ... with 2-byte loads, and each wave's weight-gradient partial builds up in its LDS row.
-// The arithmetic is the vector kernel's; the partial sums run over the block's rows in the
-// same order and the four waves are added in the same order. Only dr, each row's dot
+// (rows whose width is not a multiple of 8, views at odd offsets): lanes take columns lane,
+// lane + 64, ... with 2-byte loads. The arithmetic, the rows of each wave, the order of the
+// partial sums and of the waves' addition are the vector kernel's. Only dr, each row's dot
 // product, is summed in another order (by column residue instead of by 8-column chunk).
 template <bool EAGER>
-static __global__ void __launch_bounds__(256) rmsnorm_bwd_generic_kernel(
+static __global__ void __launch_bounds__(64 * kRmsWaves) rmsnorm_bwd_generic_kernel(
     const unsigned short* __restrict__ x, const float* __restrict__ w,
     const float* __restrict__ rstd, const unsigned short* __restrict__ dy,
     unsigned short* __restrict__ dx, float* __restrict__ dw_part, int rows, int D) {
-  extern __shared__ float lds_part[];  // [4][D]
+  extern __shared__ float lds_part[];  // [kRmsWaves][D]
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   float* mine = lds_part + wave * D;
   for (int c = lane; c < D; c += 64) mine[c] = 0.0f;
   const int row_end = min(rows, (blockIdx.x + 1) * kRmsRowsPerBlock);
-  for (int row = blockIdx.x * kRmsRowsPerBlock + wave; row < row_end; row += 4) {
+  for (int row = blockIdx.x * kRmsRowsPerBlock + wave; row < row_end; row += kRmsWaves) {
     const float r = rstd[row];
     const unsigned short* xr = x + (long)row * D;
     const unsigned short* gr = dy + (long)row * D;
@@ -276,10 +294,7 @@ static __global__ void __launch_bounds__(256) rmsnorm_bwd_generic_kernel(
       mine[c] += pv;
     }
   }
-  __syncthreads();
-  for (int c = threadIdx.x; c < D; c += blockDim.x)
-    dw_part[(long)blockIdx.x * D + c] =
-        ((lds_part[c] + lds_part[D + c]) + lds_part[2 * D + c]) + lds_part[3 * D + c];
+  rms_block_partial(lds_part, dw_part, D);
 }
 
 // The RMSNorm backward of rows wider than 2048 columns (same arithmetic): a block of 256

@@ -73,7 +73,7 @@ extern "C" int ws_rmsnorm_forward(const void* x, const float* weight, void* y, f
                              static_cast<hipStream_t>(stream));
 }
 
-// Rows per block of the RMSNorm backward: 32 for rows of up to 2048 columns (4 waves, one
+// Rows per block of the RMSNorm backward: 32 for rows of up to 2048 columns (8 waves, one
 // row each at a time); for wider rows (one row per block at a time) the largest power of two
 // from 4 to 32 that still gives at least 512 blocks (measured against 256 and 1024 at
 // 4096 to 8192 columns: 512 blocks was fastest or tied at every shape).
@@ -91,10 +91,11 @@ extern "C" int64_t ws_rmsnorm_backward_partial_floats(int64_t rows, int64_t d) {
 template <int SEGS>
 static int launch_rms_bwd(const void* x, const float* weight, const float* rstd, const void* grad,
                           void* dx, float* partial, int rows, int d, int eager, hipStream_t s) {
-  const int lds = 4 * d * (int)sizeof(float);
+  // The waves' partial rows, and for the vector kernel the weight row.
+  const int lds = (kRmsWaves + (SEGS > 0 ? 1 : 0)) * d * (int)sizeof(float);
   auto launch = [&](auto kernel) {
     if (int rc = ensure_lds(reinterpret_cast<const void*>(kernel), lds)) return rc;
-    hipLaunchKernelGGL(kernel, dim3(cdiv(rows, kRmsRowsPerBlock)), dim3(256), lds, s,
+    hipLaunchKernelGGL(kernel, dim3(cdiv(rows, kRmsRowsPerBlock)), dim3(64 * kRmsWaves), lds, s,
                        static_cast<const unsigned short*>(x), weight, rstd,
                        static_cast<const unsigned short*>(grad), static_cast<unsigned short*>(dx),
                        partial, rows, d);
