@@ -40,7 +40,8 @@ int device_cus() {
 
 // hipFuncSetAttribute applies to the current device. The limit set for each (kernel,
 // device) is remembered and only ever raised: a kernel whose LDS size depends on its
-// arguments (the RMSNorm backward's [4][d] partials) may come first with a small size.
+// arguments (the RMSNorm backward's per-wave partial rows of d floats) may come first
+// with a small size.
 int ensure_lds(const void* kernel, int bytes) {
   struct Limit {
     const void* kernel;
