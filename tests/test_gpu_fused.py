@@ -516,7 +516,8 @@ def test_standalone_swiglu_forward_backward(shape, eager_rounding):
     assert_bf16_close(actual.grad.reshape(-1, shape[-1]), want, "swiglu grad")
 
 
-@pytest.mark.parametrize("shape", [(3, 24), (2, 16, 128), (257, 2048)])
+@pytest.mark.parametrize("shape", [(3, 24), (2, 16, 128), (257, 2048), (1, 2048), (39, 1024),
+                                   (100, 512), (65, 1536), (8, 2000), (4, 40, 1000)])
 def test_standalone_rmsnorm_forward_backward(shape):
     from ops.activation_execution import bf16_rmsnorm
 
