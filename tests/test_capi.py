@@ -152,3 +152,14 @@ def test_rmsnorm_backward_partial_rows_per_width():
     assert q(4096, 8192) == 512 * 8192    # 8 rows per block
     assert q(1000, 2056) == 250 * 2056    # 4 rows per block (fewer than 512 blocks)
     assert q(65536, 4096) == 2048 * 4096  # 32 rows per block
+
+
+def test_transpose_refuses_shapes_beyond_its_grid_before_any_launch():
+    """The weight transpose runs 64-row blocks along the grid's y dimension; more rows than
+    65535 blocks cover are refused with an error before any device call, as are strides
+    shorter than a row."""
+    gpu_ptr = 1 << 20  # never dereferenced
+    with pytest.raises(RuntimeError, match="exceeds 4194240"):
+        _hip.call("ws_transpose_bf16", gpu_ptr, 8, gpu_ptr, 65535 * 64 + 1, 8, None)
+    with pytest.raises(RuntimeError, match="invalid transpose shape"):
+        _hip.call("ws_transpose_bf16", gpu_ptr, 4, gpu_ptr, 8, 8, None)

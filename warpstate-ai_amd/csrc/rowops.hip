@@ -242,6 +242,9 @@ extern "C" int ws_transpose_bf16(const void* in, int64_t ld_in, void* out, int64
   if (!in || !out) return set_error(kInvalid, "null pointer");
   if (rows < 1 || cols < 1 || !fits_i32(rows) || !fits_i32(cols) || ld_in < cols)
     return set_error(kInvalid, "invalid transpose shape");
+  // Row blocks of 64 run along the grid's y dimension (at most 65535 blocks).
+  if (cdiv(rows, 64) > 65535)
+    return set_error(kInvalid, "transpose of %ld rows exceeds 4194240", (long)rows);
   const unsigned long pi = reinterpret_cast<unsigned long>(in), po = reinterpret_cast<unsigned long>(out);
   const int vec = rows % 8 == 0 && cols % 8 == 0 && ld_in % 8 == 0 && pi % 16 == 0 && po % 16 == 0;
   if (vec) {
