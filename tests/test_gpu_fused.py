@@ -863,3 +863,40 @@ def test_cross_entropy_combine_and_logit_gradient_entry_points():
     want = ((soft - onehot) * (0.5 / count) * valid.unsqueeze(1)).bfloat16()
     assert_bf16_close(out, want, "logit gradients")
     assert torch.count_nonzero(out.cpu()[~valid]).item() == 0
+
+
+@pytest.mark.parametrize("rows,cols,gate", [(16384, 9216, (6144, 8192)), (37, 80, (13, 61)),
+                                            (1000, 264, (0, 264)), (3, 24, (8, 8)),
+                                            (257, 1032, (515, 1029))])
+@pytest.mark.parametrize("mode", ["in_place", "out_of_place", "unaligned"])
+def test_sigmoid_backward_cols_bits(rows, cols, gate, mode):
+    """dP = r((dout (1 - s)) s) on the gate columns and dout elsewhere, bit for bit against
+    the same FP32 expression on the CPU: in place (only the gate columns' 8-column groups
+    are touched, the others keep their bits), into a fresh buffer, and with views 2 bytes
+    off a 16-byte boundary (the one-element path)."""
+    from ops.fused_execution import sigmoid_backward_cols
+
+    gen = _gen(31)
+    dout = (torch.randn(rows, cols, generator=gen) * 1e-2).bfloat16()
+    s = torch.rand(rows, cols, generator=gen).bfloat16()
+    lo, hi = gate
+    want = dout.clone()
+    g, sv = dout[:, lo:hi].float(), s[:, lo:hi].float()
+    want[:, lo:hi] = ((g * (1.0 - sv)) * sv).bfloat16()
+    print(f"sigmoid backward {rows}x{cols} gate={gate} {mode}", flush=True)
+    if mode == "unaligned":
+        def shifted(t):
+            buf = torch.empty(t.numel() + 8, dtype=t.dtype, device="cuda")
+            view = buf[1:1 + t.numel()].view(t.shape)
+            view.copy_(t.cuda())
+            return view
+        d, o = shifted(dout), shifted(s)
+        got = sigmoid_backward_cols(d, o, gate)
+    elif mode == "in_place":
+        d = dout.cuda()
+        got = sigmoid_backward_cols(d, s.cuda(), gate, d)
+        assert got.data_ptr() == d.data_ptr()
+    else:
+        got = sigmoid_backward_cols(dout.cuda(), s.cuda(), gate)
+    torch.cuda.synchronize()
+    assert torch.equal(got.cpu().view(torch.int16), want.view(torch.int16))
